@@ -1,0 +1,253 @@
+"""GPU parity: the HIP kernels, called through the C ABI (libattn_flash.so), against the CPU
+oracle on identical bf16 bit patterns, with the reference's pass rule
+nbad == 0 and max|O - O_ref| <= 8e-3 * max|O_ref| over the checked rows (flash.c:935-980).
+
+Outputs are poisoned with NaN before each call, so an unwritten row is a failure. Large
+configurations check the reference's spread rows (flash.c:900-913), which always include
+row Sq-1 (every key block and every rescale)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import transfer_station_amd as ts
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+NT = min(16, os.cpu_count() or 1)
+SEED0 = 0x12345678
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu_present():
+    n = ts.device_count()
+    assert n >= 1, "no HIP device visible: GPU tests must run on the MI355X box"
+
+
+def check(oracle, name, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk=128, ref_cap=0, O=None):
+    say("case %s: Hq=%d Hkv=%d Sq=%d Sk=%d D=%d causal=%d bk=%d" % (name, Hq, Hkv, Sq, Sk, D,
+                                                                     causal, bk))
+    if O is None:
+        O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+    rows = oracle.ref_rowset(Sq, ref_cap)
+    R = oracle.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, rows, nthreads=NT)
+    ok, mad, maxref, nbad = oracle.cmp_rows(R, O, Hq, Sq, D, rows)
+    say("   err/scale=%.2e nbad=%d -> %s" % (mad / maxref if maxref else 0.0, nbad,
+                                            "PASS" if ok else "FAIL"))
+    assert ok, (name, mad, maxref, nbad)
+    return O
+
+
+# ---- the reference's short suite (LCG data, every row) ---------------------------------------
+SUITE = [
+    ("MHA prefill", 4, 4, 8, 8, 64, 0),
+    ("MHA prefil.causal", 4, 4, 8, 8, 64, 1),
+    ("GQA prefill", 8, 2, 8, 8, 64, 0),
+    ("GQA prefil.causal", 8, 2, 8, 8, 64, 1),
+    ("MHA decode(Sq=1)", 4, 4, 1, 16, 64, 0),
+    ("GQA decode(Sq=1)", 8, 2, 1, 16, 64, 0),
+    ("MQA prefill", 8, 1, 8, 8, 64, 0),
+    ("odd + multiblock", 6, 3, 130, 70, 40, 1),
+    ("GQA big head_dim", 8, 2, 4, 12, 128, 0),
+]
+
+
+@pytest.mark.parametrize("bk", [16, 32, 64, 128, 256, 4096])
+@pytest.mark.parametrize("case", SUITE, ids=[c[0] for c in SUITE])
+def test_reference_suite(oracle, case, bk):
+    name, Hq, Hkv, Sq, Sk, D, causal = case
+    Q, K, V = ts.synth_lcg_qkv(Hq, Hkv, Sq, Sk, D)
+    check(oracle, name, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+
+
+def test_golden_fixtures_direct():
+    import json
+    from oracle import oracle as o
+    man = json.load(open(os.path.join(GOLD, "manifest.json")))
+    for m in man:
+        z = np.load(os.path.join(GOLD, m["file"]))
+        if m["data"] == "lcg":
+            Q, K, V = o.lcg_qkv(m["Hq"], m["Hkv"], m["Sq"], m["Sk"], m["D"], m["seed"])
+        else:
+            Q, K, V = z["Q"], z["K"], z["V"]
+        say("fixture %s" % m["name"])
+        O = ts.run_attention(Q, K, V, m["Hq"], m["Hkv"], m["Sq"], m["Sk"], m["D"], m["causal"])
+        G = z["O"]
+        assert np.isfinite(O).all()
+        err = np.abs(O - G).max() / np.abs(G).max()
+        say("   err/scale vs float64 = %.2e" % err)
+        assert err <= 8e-3, m["name"]
+
+
+# ---- the BASELINE configurations ---------------------------------------------------------------
+def test_c1_mha_256(oracle):
+    Q, K, V = ts.synth_normal_qkv(4, 4, 256, 256, 64, SEED0 + 1)
+    check(oracle, "c1 MHA", Q, K, V, 4, 4, 256, 256, 64, 0, 128)
+
+
+def test_c2_gqa_decode(oracle):
+    B, Hq, Hkv, Sk, D = 64, 32, 8, 4096, 128
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, 1, Sk, D, SEED0 + 2)
+    check(oracle, "c2 GQA decode", Q, K, V, B * Hq, B * Hkv, 1, Sk, D, 0, 128)
+
+
+@pytest.mark.parametrize("Hkv,Sk", [(8, 4096), (8, 1000), (2, 777), (1, 64)])
+def test_decode_split_paths(oracle, Hkv, Sk):
+    """Few kv heads -> the key range is split over workgroups and merged (attn_merge_kernel)."""
+    Hq, D = Hkv * 4, 128
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, 1, Sk, D, SEED0 + 20 + Sk)
+    check(oracle, "decode split", Q, K, V, Hq, Hkv, 1, Sk, D, 0, 128)
+    # g*Sq = 16 rows: the largest query block the decode tile holds, causal
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, 4, Sk, D, SEED0 + 21 + Sk)
+    check(oracle, "decode split causal Sq=4", Q, K, V, Hq, Hkv, 4, Sk, D, 1, 128)
+
+
+@pytest.mark.parametrize("S", [1024, 2048, 4096])
+def test_c3_gqa_prefill(oracle, S):
+    B, Hq, Hkv, D = 4, 32, 8, 128
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, S, S, D, SEED0 + 3)
+    check(oracle, "c3 GQA prefill %d" % S, Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128, ref_cap=8)
+
+
+def test_c4_mqa_prefill(oracle):
+    B, Hq, Hkv, S, D = 8, 16, 1, 2048, 128
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, S, S, D, SEED0 + 4)
+    check(oracle, "c4 MQA prefill", Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128, ref_cap=8)
+
+
+@pytest.mark.parametrize("bk", [32, 64, 128, 256, 512])
+def test_c5_ragged_softmax_stress(oracle, bk):
+    B, Hq, Hkv, Sq, Sk, D = 2, 24, 6, 1000, 4000, 64
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, Sq, Sk, D, SEED0 + 5, sigma_q=4.0)
+    check(oracle, "c5 ragged", Q, K, V, B * Hq, B * Hkv, Sq, Sk, D, 0, bk, ref_cap=16)
+
+
+def test_qwen3_causal_long(oracle):
+    """The reference's --long case shape (flash.c:1312-1314) at 1k, causal, spread rows."""
+    Q, K, V = ts.synth_lcg_qkv(16, 8, 1024, 1024, 128)
+    check(oracle, "qwen3 1k causal", Q, K, V, 16, 8, 1024, 1024, 128, 1, 128, ref_cap=8)
+
+
+# ---- tails, head_dim, masks -----------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [0, 1])
+@pytest.mark.parametrize("bk", [32, 64, 128])
+def test_tail_probe(oracle, bk, causal):
+    for Sk in (1, bk - 1, bk, bk + 1, 2 * bk, 2 * bk + 1, 70):
+        for Sq in (40, 1):
+            Q, K, V = ts.synth_lcg_qkv(4, 2, Sq, Sk, 64)
+            check(oracle, "tail", Q, K, V, 4, 2, Sq, Sk, 64, causal, bk)
+
+
+@pytest.mark.parametrize("D", [1, 2, 3, 7, 8, 16, 24, 33, 40, 63, 64, 65, 72, 100, 127, 128])
+def test_head_dim_sweep(oracle, D):
+    for Sq, Hq, Hkv in ((37, 4, 2), (1, 8, 2)):
+        Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, 150, D, 1000 + D)
+        check(oracle, "D sweep", Q, K, V, Hq, Hkv, Sq, 150, D, 1, 64)
+
+
+def test_sk_one_copies_v(oracle):
+    """Sk = 1: a one-element softmax. The kernels evaluate p = 2^(s*c - m*c) with one fma, so
+    p at the row max is 1 within 2^-23 (not exactly 1, unlike the reference's exp(s - m)):
+    O equals V[0] to within a few ulp (and bf16(p) == 1 exactly)."""
+    for Sq in (1, 50):
+        Q, K, V = ts.synth_normal_qkv(8, 2, Sq, 1, 128, 7)
+        O = ts.run_attention(Q, K, V, 8, 2, Sq, 1, 128, 0).reshape(8, Sq, 128)
+        Vf = oracle.bf16_to_f32(V).reshape(2, 128)
+        for h in range(8):
+            want = np.broadcast_to(Vf[h // 4], (Sq, 128))
+            assert np.all(np.abs(O[h] - want) <= 2.0 ** -21 * np.abs(want))
+
+
+def test_fully_masked_causal_rows_are_zero():
+    Q, K, V = ts.synth_lcg_qkv(6, 3, 130, 70, 40)
+    O = ts.run_attention(Q, K, V, 6, 3, 130, 70, 40, 1).reshape(6, 130, 40)
+    assert np.all(O[:, :60] == 0.0) and np.isfinite(O).all()
+    Q, K, V = ts.synth_normal_qkv(8, 2, 300, 20, 128, 8)
+    O = ts.run_attention(Q, K, V, 8, 2, 300, 20, 128, 1).reshape(8, 300, 128)
+    assert np.all(O[:, :280] == 0.0) and np.all(np.abs(O[:, 280:]).max(axis=2) > 0)
+
+
+# ---- invariants (GPU against GPU) ------------------------------------------------------------------
+def test_gqa_equals_mha_with_repeated_kv_bitwise():
+    Hq, Hkv, Sq, Sk, D = 16, 4, 200, 333, 128
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 11)
+    g = Hq // Hkv
+    Kr = np.repeat(K.reshape(Hkv, 1, -1), g, axis=1).reshape(-1)
+    Vr = np.repeat(V.reshape(Hkv, 1, -1), g, axis=1).reshape(-1)
+    for causal in (0, 1):
+        a = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal)
+        b = ts.run_attention(Q, Kr, Vr, Hq, Hq, Sq, Sk, D, causal)
+        assert np.array_equal(a, b)
+
+
+def test_batch_fold_bitwise_and_determinism():
+    B, Hq, Hkv, Sq, Sk, D = 3, 8, 2, 150, 260, 64
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, Sq, Sk, D, 12)
+    folded = ts.run_attention(Q, K, V, B * Hq, B * Hkv, Sq, Sk, D, 1)
+    again = ts.run_attention(Q, K, V, B * Hq, B * Hkv, Sq, Sk, D, 1)
+    assert np.array_equal(folded, again)  # run-to-run bitwise (no LDS races)
+    nq, nk = Hq * Sq * D, Hkv * Sk * D
+    for b in range(B):
+        one = ts.run_attention(Q[b * nq:(b + 1) * nq], K[b * nk:(b + 1) * nk],
+                               V[b * nk:(b + 1) * nk], Hq, Hkv, Sq, Sk, D, 1)
+        assert np.array_equal(folded[b * nq:(b + 1) * nq], one)
+
+
+def test_key_permutation_invariance(oracle):
+    Hq, Hkv, Sq, Sk, D = 4, 2, 64, 500, 64
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 13)
+    perm = np.random.default_rng(0).permutation(Sk)
+    Kp = K.reshape(Hkv, Sk, D)[:, perm].reshape(-1).copy()
+    Vp = V.reshape(Hkv, Sk, D)[:, perm].reshape(-1).copy()
+    a = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0)
+    b = ts.run_attention(Q, Kp, Vp, Hq, Hkv, Sq, Sk, D, 0)
+    rows = np.arange(Sq, dtype=np.int32)
+    assert oracle.cmp_rows(a, b, Hq, Sq, D, rows)[0]
+
+
+def test_bk_invariance(oracle):
+    Hq, Hkv, Sq, Sk, D = 8, 2, 300, 1000, 128
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 14)
+    base = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 1, 128)
+    rows = np.arange(Sq, dtype=np.int32)
+    for bk in (16, 32, 64, 256, 1024, 4096):
+        other = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 1, bk)
+        assert oracle.cmp_rows(base, other, Hq, Sq, D, rows)[0], bk
+
+
+# ---- the other entry points ------------------------------------------------------------------------
+def test_pack_v_full_transposes_exactly():
+    Hkv, Sk, D = 3, 77, 40
+    V = np.arange(Hkv * Sk * D, dtype=np.uint16)
+    with ts.DeviceBuffer.from_array(V) as dv, ts.DeviceBuffer(V.nbytes) as dp:
+        ts.pack_v_full(dv, dp, Hkv, Sk, D)
+        ts.synchronize()
+        got = dp.download(np.uint16).reshape(Hkv, D, Sk)
+    assert np.array_equal(got, V.reshape(Hkv, Sk, D).transpose(0, 2, 1))
+
+
+def test_timing_struct_and_scratch_reuse(oracle):
+    Hq, Hkv, Sq, Sk, D = 8, 2, 1, 2048, 128
+    bk_max = 4096
+    sbytes = ts.attn_flash_scratch_bytes(D, bk_max)
+    tm = ts.AttnTimes()
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 15)
+    rows = np.arange(Sq, dtype=np.int32)
+    R = oracle.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, rows)
+    with ts.DeviceBuffer(sbytes) as ds, ts.DeviceBuffer.from_array(Q) as dq, \
+            ts.DeviceBuffer.from_array(K) as dk, ts.DeviceBuffer.from_array(V) as dv, \
+            ts.DeviceBuffer(Hq * Sq * D * 4) as do:
+        ds.fill_bytes(0xFF)  # poisoned scratch: the kernels must initialise what they read
+        for bk in (64, 512, 4096, 16):  # one scratch sized for the largest bk serves all
+            do.fill_bytes(0xFF)
+            ts.attn_flash(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, 0, bk, ds, 0, tm)
+            O = do.download(np.float32)
+            assert oracle.cmp_rows(R, O, Hq, Sq, D, rows)[0], bk
+    assert tm.qxk > 0 and tm.packv == 0 and tm.softmax == 0 and tm.sxv == 0

@@ -1,0 +1,616 @@
+// attn_kernels.hip -- gfx950 (CDNA4) kernels for the bf16 flash-attention forward.
+//
+// Semantics follow the reference's attn_flash (liujiang833/transfer_station flash.c:727-864):
+// kv = h / (Hq/Hkv) (flash.c:765,780); scores scale*Q.K with scale = 1/sqrtf(D) (flash.c:766);
+// bottom-right causal mask j <= Sk-Sq+i (flash.c:783,535-543); online softmax per key block with
+// alpha = exp(m_old - m_new), 0 on a row's first contributing block, state held on a fully
+// masked block (flash.c:546-559); P rounded RNE to bf16 before P.V while l sums the unrounded
+// fp32 p (flash.c:566-576); O = acc * (l > 0 ? 1/l : 0) for every row (flash.c:851-860).
+// The implementation is this file's own: MFMA tiles, LDS staging and register-resident softmax.
+//
+// Exponentials run in the log2 domain: with c = scale*log2(e) and scores kept as raw dot
+// products s, p = 2^(s*c - m*c) equals e^(scale*s - scale*m).
+//
+// Kernels:
+//   attn_prefill_kernel<DP,KT,CAUSAL,VEC>  MFMA prefill; one workgroup = 4 waves x 32 query rows
+//   attn_decode_kernel<DP,CAUSAL,VEC>      split-K decode for g*Sq <= 16 rows per kv head
+//   attn_merge_kernel                      log-sum-exp merge of the decode partials
+//   attn_pack_v_kernel                     V [Hkv][Sk][D] -> V^T [Hkv][D][Sk]
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kNegInf = -__builtin_inff();
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Remap the
+// hardware block id so that consecutive logical ids land on the same XCD: logical ids that
+// share a kv head then share that XCD's L2 copy of K/V.
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+    const int per = n >> 3, rem = n & 7;
+    const int x = b & 7, i = b >> 3;
+    return (x < rem) ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
+__device__ __forceinline__ u32x4 zero4() {
+    u32x4 z = {0u, 0u, 0u, 0u};
+    return z;
+}
+
+// Eight consecutive bf16 of one row, columns [col, col+8), zero-filled past D or when !ok.
+// VEC requires D % 8 == 0 and a 16-byte aligned base, so one 16-byte load covers them.
+template <bool VEC>
+__device__ __forceinline__ u32x4 load_row8(const uint16_t *base, size_t row, int col, int D,
+                                           bool ok) {
+    if (!ok || col >= D)
+        return zero4();
+    const uint16_t *p = base + row * (size_t)D + col;
+    if (VEC)
+        return *reinterpret_cast<const u32x4 *>(p);
+    uint32_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        e[j] = (col + j < D) ? (uint32_t)p[j] : 0u;
+    u32x4 r = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ bf16x8 join_tr(s16x4 lo, s16x4 hi) {
+    typedef __attribute__((ext_vector_type(8))) short s16x8;
+    s16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element r (r = 0..3) from
+// row (4r + i/4) of the group's 16x4 matrix of 8-byte reads, element i%4. Lanes that address
+// V[key0 + j/4][d0 + 4*(j%4)] therefore receive V[key0 + r][d0 + i]: four keys for one column.
+__device__ __forceinline__ s16x4 lds_read_tr(const uint16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(p));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ void lds_wave_fence() {
+    // Wave-private LDS reuse: finish this wave's outstanding LDS traffic and keep the compiler
+    // from moving LDS accesses across this point.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// ------------------------------------------------------------------------------------------
+// Prefill. Workgroup = 4 waves; wave w owns query rows q0 = qt*128 + 32w .. +31 of query head h.
+// Per key tile of KT keys (one online-softmax update per tile):
+//   S^T[key][q] = K_tile . Q^T     (v_mfma_f32_32x32x16_bf16, A = K rows from LDS, B = Q regs)
+//   each lane holds one query (q = lane%32) and 16 keys per 32-key sub-tile, so the row max is
+//   an in-lane reduction plus one exchange with lane^32;
+//   O^T[d][q] += V^T . P^T         (A = V^T via ds_read_b64_tr_b16 from row-major LDS,
+//                                    B = P^T straight from the S^T registers)
+// The S^T operand rows are permuted (bits 2 and 3 of the row swapped within each 16-row half)
+// so that a lane's 8 P values for one 16-key MFMA step are 8 consecutive keys.
+// ------------------------------------------------------------------------------------------
+template <int DP, int KT, bool CAUSAL, bool VEC>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+    const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
+    float c, int nqt) {
+    static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
+    constexpr int KSTR = DP + 8;  // LDS row stride (elements) of K: 16-byte pad
+    constexpr int VSTR = DP + 16; // LDS row stride of V: 32-byte pad
+    constexpr int NCH = KT * DP / 8 / 256; // 16-byte chunks per thread per tile, per tensor
+    static_assert(NCH >= 1 && (KT * DP / 8) % 256 == 0, "chunking");
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * VSTR];
+
+    const int g = Hq / Hkv;
+    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int u = L / (g * nqt);
+    const int rr = L - u * (g * nqt);
+    const int qt = rr / g;
+    const int h = u * g + (rr - qt * g);
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int q0 = qt * 128 + w * 32;
+    const int myq = q0 + l32;
+
+    const uint16_t *Qh = Q + (size_t)h * Sq * D;
+    const uint16_t *Kh = K + (size_t)u * Sk * D;
+    const uint16_t *Vh = V + (size_t)u * Sk * D;
+
+    // Q as the B operand: lane holds Q[myq][16kk + 8hi .. +7].
+    bf16x8 qb[DP / 16];
+#pragma unroll
+    for (int kk = 0; kk < DP / 16; ++kk)
+        qb[kk] = as_bf16x8(load_row8<VEC>(Qh, (size_t)myq, kk * 16 + hi * 8, D, myq < Sq));
+
+    // Key tiles this workgroup needs, and the last key any row of this wave may attend.
+    int nkt = (Sk + KT - 1) / KT;
+    int wave_maxkey = (q0 < Sq) ? Sk - 1 : -1;
+    if (CAUSAL) {
+        const int last_row = min(qt * 128 + 127, Sq - 1);
+        const int maxkey = Sk - Sq + last_row;
+        nkt = (maxkey < 0) ? 0 : min(nkt, maxkey / KT + 1);
+        if (q0 < Sq)
+            wave_maxkey = min(Sk - 1, Sk - Sq + min(q0 + 31, Sq - 1));
+    }
+    const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + myq) : Sk - 1;
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x16 o[DP / 32];
+#pragma unroll
+    for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            o[db][i] = 0.f;
+
+    u32x4 kr[NCH], vr[NCH];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            const int cidx = tid + 256 * r;
+            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+            const int key = kt * KT + row;
+            kr[r] = load_row8<VEC>(Kh, (size_t)key, col, D, key < Sk);
+            vr[r] = load_row8<VEC>(Vh, (size_t)key, col, D, key < Sk);
+        }
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            const int cidx = tid + 256 * r;
+            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+            *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
+            *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+        }
+    };
+
+    // Row of the K tile this lane feeds to the S^T MFMA (bits 2,3 of l32 swapped).
+    const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int g16 = lane >> 4, i16 = lane & 15;
+
+    if (nkt > 0) {
+        gload(0);
+        swrite(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nkt)
+            gload(kt + 1);
+        const int kbase = kt * KT;
+        if (kbase <= wave_maxkey) {
+            f32x16 s[KT / 32];
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    s[t][i] = 0.f;
+                const uint16_t *kb = &Ks[buf][(t * 32 + kperm) * KSTR + hi * 8];
+#pragma unroll
+                for (int kk = 0; kk < DP / 16; ++kk) {
+                    const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb + kk * 16));
+                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[kk], s[t], 0, 0, 0);
+                }
+            }
+            // Register (t, i) of this lane holds key kbase + 32t + 16(i/8) + 8hi + i%8.
+            const bool need_mask =
+                (kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + q0);
+            if (need_mask) {
+#pragma unroll
+                for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kbase + t * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
+                        if (key > lim)
+                            s[t][i] = kNegInf;
+                    }
+            }
+            float mx = kNegInf;
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    mx = fmaxf(mx, s[t][i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(m_run, mx);
+            const float muse = (mnew == kNegInf) ? 0.f : mnew;
+            const float alpha = fast_exp2((m_run - muse) * c);
+            const float mc = muse * c;
+            float psum = 0.f;
+            bf16x8 pk[KT / 16];
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = fast_exp2(fmaf(s[t][i], c, -mc));
+                    psum += p;
+                    pk[2 * t + (i >> 3)][i & 7] = (__bf16)p;
+                }
+            l_run = alpha * l_run + psum;
+            m_run = mnew;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    o[db][i] *= alpha;
+#pragma unroll
+            for (int cc = 0; cc < KT / 16; ++cc) {
+                const uint16_t *vb =
+                    &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR + (g16 & 1) * 16 + 4 * (i16 & 3)];
+#pragma unroll
+                for (int db = 0; db < DP / 32; ++db) {
+                    const bf16x8 a = join_tr(lds_read_tr(vb + db * 32), lds_read_tr(vb + db * 32 + 4 * VSTR));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < nkt)
+            swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
+    if (myq < Sq) {
+        float *orow = O + ((size_t)h * Sq + myq) * D;
+        // O^T register (db, i) of this lane holds d = 32db + 8(i/4) + 4hi + i%4.
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int d = db * 32 + i4 * 8 + 4 * hi;
+                f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
+                           o[db][4 * i4 + 3] * inv};
+                if (VEC) {
+                    if (d < D)
+                        *reinterpret_cast<f32x4 *>(orow + d) = v;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (d + j < D)
+                            orow[d + j] = v[j];
+                }
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Decode (split-K). One workgroup per (kv head u, split sp) serves all M = g*Sq <= 16 query
+// rows of that kv head from ONE read of its K/V range [sp*kps, min(sp*kps+kps, Sk)). Waves
+// take interleaved 32-key tiles; per tile (v_mfma_f32_16x16x32_bf16):
+//   S^T[key][row] = K . Q^T  (A = K rows loaded from global straight into the operand layout)
+//   O^T[d][row]  += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from a wave-private LDS tile)
+// The 4 waves merge in LDS; the workgroup writes O directly (nsplit == 1) or one partial
+// (m, l, acc[D]) per row into the caller's scratch for attn_merge_kernel.
+// ------------------------------------------------------------------------------------------
+template <int DP, bool CAUSAL, bool VEC>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+    const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
+    float *__restrict__ pl, float *__restrict__ pacc, int Hq, int Hkv, int Sq, int Sk, int D,
+    float c, int nsplit, int kps) {
+    constexpr int VSTR = DP + 16;
+    constexpr int VNCH = 32 * DP / 8 / 64; // 16-byte chunks per lane per V tile
+    constexpr int VTILE = 32 * VSTR;       // elements of one wave's V tile
+    __shared__ __attribute__((aligned(16))) uint16_t Vw[4 * VTILE];
+    __shared__ float red_m[4][16], red_l[4][16];
+    // The 4-wave merge reuses the V tiles' memory as float [4][16][DP].
+    static_assert(4 * 16 * DP * 4 <= 4 * VTILE * 2, "merge area must fit in the V tiles");
+
+    const int g = Hq / Hkv, M = g * Sq;
+    const int u = (int)blockIdx.x / nsplit, sp = (int)blockIdx.x % nsplit;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int r16 = lane & 15, grp = lane >> 4;
+    const int k0 = sp * kps, k1 = min(k0 + kps, Sk);
+
+    const bool rvalid = r16 < M;
+    const int gi = rvalid ? r16 / Sq : 0, qi = rvalid ? r16 % Sq : 0;
+    const int h = u * g + gi;
+    const uint16_t *Kh = K + (size_t)u * Sk * D;
+    const uint16_t *Vh = V + (size_t)u * Sk * D;
+
+    bf16x8 qb[DP / 32];
+#pragma unroll
+    for (int kk = 0; kk < DP / 32; ++kk)
+        qb[kk] = as_bf16x8(
+            load_row8<VEC>(Q + (size_t)h * Sq * D, (size_t)qi, kk * 32 + grp * 8, D, rvalid));
+    const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + qi) : Sk - 1;
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x4 o[DP / 16];
+#pragma unroll
+    for (int db = 0; db < DP / 16; ++db)
+        o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint16_t *vt = &Vw[w * VTILE];
+    for (int tb = k0 + w * 32; tb < k1; tb += 128) {
+        u32x4 ka[2][DP / 32];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
+#pragma unroll
+            for (int kk = 0; kk < DP / 32; ++kk)
+                ka[t][kk] = load_row8<VEC>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+        }
+        u32x4 vv[VNCH];
+#pragma unroll
+        for (int r = 0; r < VNCH; ++r) {
+            const int cidx = lane + 64 * r;
+            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+            vv[r] = load_row8<VEC>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
+        }
+        lds_wave_fence(); // previous tile's transposed reads are complete
+#pragma unroll
+        for (int r = 0; r < VNCH; ++r) {
+            const int cidx = lane + 64 * r;
+            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+            *reinterpret_cast<u32x4 *>(&vt[row * VSTR + col]) = vv[r];
+        }
+        f32x4 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < DP / 32; ++kk)
+                s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][kk]), qb[kk], s[t], 0,
+                                                               0, 0);
+        }
+        // Register (t, i) of this lane holds key tb + 8grp + 4t + i for row r16.
+        float mx = kNegInf;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = tb + 8 * grp + 4 * t + i;
+                if (key >= k1 || key > lim)
+                    s[t][i] = kNegInf;
+                mx = fmaxf(mx, s[t][i]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = fmaxf(m_run, mx);
+        const float muse = (mnew == kNegInf) ? 0.f : mnew;
+        const float alpha = fast_exp2((m_run - muse) * c);
+        const float mc = muse * c;
+        float psum = 0.f;
+        bf16x8 pk;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float p = fast_exp2(fmaf(s[t][i], c, -mc));
+                psum += p;
+                pk[4 * t + i] = (__bf16)p;
+            }
+        l_run = alpha * l_run + psum;
+        m_run = mnew;
+#pragma unroll
+        for (int db = 0; db < DP / 16; ++db)
+            o[db] *= alpha;
+        lds_wave_fence(); // this tile's V is in LDS before the transposed reads
+        const uint16_t *vb = &vt[(8 * grp + (r16 >> 2)) * VSTR + 4 * (r16 & 3)];
+#pragma unroll
+        for (int db = 0; db < DP / 16; ++db) {
+            const bf16x8 a = join_tr(lds_read_tr(vb + db * 16), lds_read_tr(vb + db * 16 + 4 * VSTR));
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
+        }
+    }
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+
+    // Merge the 4 waves: O^T register (db, i) of this lane holds d = 16db + 4grp + i, row r16.
+    __syncthreads();
+    float *om = reinterpret_cast<float *>(Vw); // [4][16][DP]
+    if (grp == 0) {
+        red_m[w][r16] = m_run;
+        red_l[w][r16] = l_run;
+    }
+#pragma unroll
+    for (int db = 0; db < DP / 16; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            om[(w * 16 + r16) * DP + db * 16 + 4 * grp + i] = o[db][i];
+    __syncthreads();
+    for (int idx = tid; idx < M * D; idx += 256) {
+        const int r = idx / D, d = idx - r * D;
+        float mx = kNegInf;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww)
+            mx = fmaxf(mx, red_m[ww][r]);
+        const float muse = (mx == kNegInf) ? 0.f : mx;
+        float acc = 0.f, lsum = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float wgt = fast_exp2((red_m[ww][r] - muse) * c);
+            acc += wgt * om[(ww * 16 + r) * DP + d];
+            lsum += wgt * red_l[ww][r];
+        }
+        const int hr = u * g + r / Sq, qr = r % Sq;
+        const size_t orow = (size_t)hr * Sq + qr;
+        if (nsplit == 1) {
+            O[orow * D + d] = acc * ((lsum > 0.f) ? 1.0f / lsum : 0.f);
+        } else {
+            const size_t slot = orow * nsplit + sp;
+            pacc[slot * D + d] = acc;
+            if (d == 0) {
+                pm[slot] = mx;
+                pl[slot] = lsum;
+            }
+        }
+    }
+}
+
+// Merge of split-K partials: one workgroup per output row (h*Sq + i).
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ pm,
+                                                         const float *__restrict__ pl,
+                                                         const float *__restrict__ pacc,
+                                                         float *__restrict__ O, int D, int nsplit,
+                                                         float c) {
+    const size_t row = blockIdx.x;
+    const float *m = pm + row * nsplit;
+    const float *l = pl + row * nsplit;
+    float mx = kNegInf;
+    for (int s = 0; s < nsplit; ++s)
+        mx = fmaxf(mx, m[s]);
+    const float muse = (mx == kNegInf) ? 0.f : mx;
+    float lsum = 0.f;
+    for (int s = 0; s < nsplit; ++s)
+        lsum += fast_exp2((m[s] - muse) * c) * l[s];
+    const float inv = (lsum > 0.f) ? 1.0f / lsum : 0.f;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.f;
+        for (int s = 0; s < nsplit; ++s)
+            acc += fast_exp2((m[s] - muse) * c) * pacc[(row * nsplit + s) * D + d];
+        O[row * D + d] = acc * inv;
+    }
+}
+
+// V [Hkv][Sk][D] -> Vp [Hkv][D][Sk] through a 32x32 LDS tile (block 32x8).
+__global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__restrict__ V,
+                                                          uint16_t *__restrict__ Vp, int Sk,
+                                                          int D) {
+    __shared__ uint16_t tile[32][33];
+    const int kv = blockIdx.z;
+    const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+    const uint16_t *src = V + (size_t)kv * Sk * D;
+    uint16_t *dst = Vp + (size_t)kv * D * Sk;
+    for (int r = threadIdx.y; r < 32; r += 8) {
+        const int k = k0 + r, d = d0 + threadIdx.x;
+        tile[r][threadIdx.x] = (k < Sk && d < D) ? src[(size_t)k * D + d] : (uint16_t)0;
+    }
+    __syncthreads();
+    for (int r = threadIdx.y; r < 32; r += 8) {
+        const int d = d0 + r, k = k0 + threadIdx.x;
+        if (d < D && k < Sk)
+            dst[(size_t)d * Sk + k] = tile[threadIdx.x][r];
+    }
+}
+
+template <int DP, int KT, bool CAUSAL, bool VEC>
+hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                            int Hq, int Hkv, int Sq, int Sk, int D, float c, hipStream_t st) {
+    const int nqt = (Sq + 127) / 128;
+    const long nblk = (long)Hq * nqt;
+    if (nblk <= 0 || nblk > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_prefill_kernel<DP, KT, CAUSAL, VEC>), dim3((unsigned)nblk), dim3(256),
+                       0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt);
+    return hipGetLastError();
+}
+
+template <int DP, int KT>
+hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, float c,
+                             hipStream_t st) {
+    if (causal)
+        return vec ? launch_prefill_t<DP, KT, true, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st)
+                   : launch_prefill_t<DP, KT, true, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+    return vec ? launch_prefill_t<DP, KT, false, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st)
+               : launch_prefill_t<DP, KT, false, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+}
+
+template <int DP>
+hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                            int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int kt,
+                            float c, hipStream_t st) {
+    switch (kt) {
+    case 32:
+        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+    case 64:
+        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+    case 128:
+        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+template <int DP>
+hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                           float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
+                           int D, int causal, int vec, float c, int nsplit, int kps,
+                           hipStream_t st) {
+    const long nblk = (long)Hkv * nsplit;
+    if (nblk <= 0 || nblk > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    dim3 grid((unsigned)nblk), block(256);
+    if (causal) {
+        if (vec)
+            hipLaunchKernelGGL((attn_decode_kernel<DP, true, true>), grid, block, 0, st, Q, K, V,
+                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<DP, true, false>), grid, block, 0, st, Q, K, V,
+                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((attn_decode_kernel<DP, false, true>), grid, block, 0, st, Q, K, V,
+                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<DP, false, false>), grid, block, 0, st, Q, K,
+                               V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+// ---- extern "C" launchers called by the C host layer (attn_flash.c) -------------------------
+extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                       float *O, int Hq, int Hkv, int Sq, int Sk, int D,
+                                       int causal, int vec, int dp, int kt, float c,
+                                       void *stream) {
+    hipStream_t st = (hipStream_t)stream;
+    switch (dp) {
+    case 64:
+        return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, kt, c, st);
+    case 128:
+        return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, kt, c, st);
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+}
+
+extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                      float *O, float *pm, float *pl, float *pacc, int Hq,
+                                      int Hkv, int Sq, int Sk, int D, int causal, int vec, int dp,
+                                      float c, int nsplit, int kps, void *stream) {
+    hipStream_t st = (hipStream_t)stream;
+    switch (dp) {
+    case 64:
+        return (int)launch_decode_d<64>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal, vec,
+                                        c, nsplit, kps, st);
+    case 128:
+        return (int)launch_decode_d<128>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal,
+                                         vec, c, nsplit, kps, st);
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+}
+
+extern "C" int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc,
+                                     float *O, int rows, int D, int nsplit, float c,
+                                     void *stream) {
+    if (rows <= 0)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(128), 0,
+                       (hipStream_t)stream, pm, pl, pacc, O, D, nsplit, c);
+    return (int)hipGetLastError();
+}
+
+extern "C" int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D,
+                                      void *stream) {
+    if (Hkv <= 0 || Sk <= 0 || D <= 0 || Hkv > 65535)
+        return (int)hipErrorInvalidValue;
+    dim3 grid((unsigned)((Sk + 31) / 32), (unsigned)((D + 31) / 32), (unsigned)Hkv);
+    hipLaunchKernelGGL(attn_pack_v_kernel, grid, dim3(32, 8), 0, (hipStream_t)stream, V, Vp, Sk,
+                       D);
+    return (int)hipGetLastError();
+}
