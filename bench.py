@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X bf16 flash-attention forward (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+One step = one attn_flash call (one fused kernel launch) over the headline workload,
+BASELINE config 3 at 4k: GQA prefill B=4, Hq=32, Hkv=8, D=128, Sq=Sk=4096, non-causal,
+bf16 Q/K/V ~ N(0,1) (synthetic, seeded), fp32 O. Inputs are resident in HBM before timing;
+each timed call rotates through a pool of input copies larger than 2x the 256 MiB Infinity
+Cache, so every call streams from HBM (the reference's DDR-cold rule, flash.c:982-991).
+
+Prints ONE JSON line on stdout (diagnostics go to stderr). `value` is TFLOP/s of useful
+work 4*B*Hq*Sq*Sk*D per step over the wall-clock of the timed steps; `roofline.achieved`
+is the same work over the kernel's average duration from HIP events on its stream. The
+other BASELINE configurations (decode GB/s, 1k/2k prefill, MQA, ragged) are reported
+under "extra". The CPU baseline is the oracle (the reference's scalar fp32 attn_ref,
+restated in C) timed on a bounded spread-row sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 (published)
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E (published)
+SEED0 = 0x12345678
+INFINITY_CACHE = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(ts, B, Hq, Hkv, Sq, Sk, D, seed, sigma_q=1.0, copies=1):
+    """Upload `copies` distinct input sets (copy 0 is the config's seeded data)."""
+    bufs = []
+    for c in range(copies):
+        Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, Sq, Sk, D, seed + 0x10000 * c,
+                                      sigma_q=sigma_q)
+        bufs.append((ts.DeviceBuffer.from_array(Q), ts.DeviceBuffer.from_array(K),
+                     ts.DeviceBuffer.from_array(V), ts.DeviceBuffer(B * Hq * Sq * D * 4),
+                     (Q, K, V) if c == 0 else None))
+    return bufs
+
+
+def time_calls(ts, bufs, B, Hq, Hkv, Sq, Sk, D, causal, bk, scratch, steps, warmup):
+    """Returns (wall ms per step, HIP-event kernel ms per step)."""
+    n = len(bufs)
+    for i in range(warmup):
+        q, k, v, o, _ = bufs[i % n]
+        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch)
+    ts.synchronize()
+    e0, e1 = ts.Event(), ts.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        q, k, v, o, _ = bufs[i % n]
+        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch)
+    e1.record()
+    ts.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_ms(e1) / steps
+
+
+def parity(ts, o, bufs, B, Hq, Hkv, Sq, Sk, D, causal, ref_cap, nthreads):
+    """err/scale of copy 0 against the oracle on spread rows (reference pass rule)."""
+    Q, K, V = bufs[0][4]
+    O = bufs[0][3].download(np.float32)
+    rows = o.ref_rowset(Sq, ref_cap)
+    R = o.attn_ref(Q, K, V, B * Hq, B * Hkv, Sq, Sk, D, causal, rows, nthreads=nthreads)
+    ok, mad, maxref, nbad = o.cmp_rows(R, O, B * Hq, Sq, D, rows)
+    return {"err_over_scale": float(mad / maxref) if maxref else 0.0, "nbad": int(nbad),
+            "pass": bool(ok), "rows_checked_per_head": int(len(rows))}
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), scaled by
+    the copy-kernel calibration; read from the committed summary, or None."""
+    p = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(o, ts, budget_s=12.0):
+    """The oracle on the headline workload's rows, 1 thread and all (<=16) threads."""
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, S, S, D, SEED0 + 3)
+    flop_per_row = 4.0 * S * D
+    out = {}
+    nthreads = min(16, os.cpu_count() or 1)
+    for label, nt in (("1", 1), ("all", nthreads)):
+        # grow the row sample until the run takes a meaningful time, within the budget
+        ref_cap, heads, dt = 2, 1, 0.0
+        while True:
+            rows = o.ref_rowset(S, ref_cap)
+            t0 = time.perf_counter()
+            o.attn_ref(Q[: heads * S * D], K[: max(1, heads // 4) * S * D],
+                       V[: max(1, heads // 4) * S * D], heads, max(1, heads // 4), S, S, D, 0,
+                       rows, nthreads=nt)
+            dt = time.perf_counter() - t0
+            if dt > budget_s / 4 or ref_cap * heads >= 4096:
+                break
+            if ref_cap < 64:
+                ref_cap *= 2
+            else:
+                heads *= 2
+        nrows = len(rows) * heads
+        out[label] = {"rows": nrows, "seconds": dt, "tflops": nrows * flop_per_row / dt / 1e12,
+                      "threads": nt}
+    allc = out["all"]
+    return {"value": allc["tflops"], "unit": "TFLOP/s", "cores": allc["threads"],
+            "kind": "port",
+            "sample": "oracle attn_ref (flash.c:262-314 restated in C, gcc -O2, OpenMP over "
+                      "(head,row)) on %d spread query rows of config 3 @4k (Sk=4096, D=128), "
+                      "%.2f s; single-thread: %.4f TFLOP/s on %d rows" %
+                      (allc["rows"], allc["seconds"], out["1"]["tflops"], out["1"]["rows"]),
+            "value_1core": out["1"]["tflops"]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--bk", type=int, default=128)
+    ap.add_argument("--no-extra", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        sys.exit("bench.py: this build measures ONE GPU only (the path shards over (batch, "
+                 "kv-head) units with no communication; multi-GPU runs are not part of it)")
+
+    import transfer_station_amd as ts
+    from oracle import oracle as o
+
+    info = ts.device_info()
+    log("device:", info)
+    nthreads = min(16, os.cpu_count() or 1)
+
+    # ---- headline: config 3 @ 4k --------------------------------------------------------------
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    flops = 4.0 * B * Hq * S * S * D
+    in_bytes = (B * Hq * S * D + 2 * B * Hkv * S * D) * 2
+    copies = max(1, -(-2 * INFINITY_CACHE // in_bytes) + 0)
+    log("headline: c3 GQA prefill 4k, %d input copies (%.0f MiB each)" %
+        (copies, in_bytes / 2 ** 20))
+    bufs = make_inputs(ts, B, Hq, Hkv, S, S, D, SEED0 + 3, copies=copies)
+    scratch = ts.DeviceBuffer(ts.attn_flash_scratch_bytes(D, args.bk))
+    wall_ms, kern_ms = time_calls(ts, bufs, B, Hq, Hkv, S, S, D, 0, args.bk, scratch, args.steps,
+                                  args.warmup)
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    head_parity = parity(ts, o, bufs, B, Hq, Hkv, S, S, D, 0, 8, nthreads)
+    log("headline: %.3f ms/step wall, %.3f ms kernel -> %.1f TFLOP/s (%.1f%% of peak); %s" %
+        (wall_ms, kern_ms, achieved, 100 * achieved / MFMA_BF16_PEAK_TFLOPS, head_parity))
+    for b in bufs:
+        for x in b[:4]:
+            x.free()
+    traffic = traffic_from_profiles("attn_prefill_c3_4k_traffic.txt")
+
+    extra = {}
+    if not args.no_extra:
+        # ---- config 2: GQA decode (HBM-bound) ------------------------------------------------
+        Bd, Hqd, Hkvd, Skd, Dd = 64, 32, 8, 4096, 128
+        dbytes = (Bd * Hqd * Dd + 2 * Bd * Hkvd * Skd * Dd) * 2 + Bd * Hqd * Dd * 4
+        db = make_inputs(ts, Bd, Hqd, Hkvd, 1, Skd, Dd, SEED0 + 2, copies=1)
+        w, k = time_calls(ts, db, Bd, Hqd, Hkvd, 1, Skd, Dd, 0, args.bk, scratch, 50, 5)
+        p2 = parity(ts, o, db, Bd, Hqd, Hkvd, 1, Skd, Dd, 0, 0, nthreads)
+        extra["c2_gqa_decode"] = {"kernel_us": k * 1e3, "wall_us": w * 1e3,
+                                  "GB_s": dbytes / (k * 1e-3) / 1e9,
+                                  "hbm_frac": dbytes / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                                  "bytes_per_call": dbytes, "parity": p2}
+        log("c2 decode:", extra["c2_gqa_decode"])
+        for b in db:
+            for x in b[:4]:
+                x.free()
+        # ---- config 3 at 1k/2k, config 4, config 5, config 1 --------------------------------
+        cases = [("c3_gqa_prefill_1k", 4, 32, 8, 1024, 1024, 128, 1.0, 3, [args.bk]),
+                 ("c3_gqa_prefill_2k", 4, 32, 8, 2048, 2048, 128, 1.0, 3, [args.bk]),
+                 ("c4_mqa_prefill_2k", 8, 16, 1, 2048, 2048, 128, 1.0, 4, [args.bk]),
+                 ("c5_ragged_gqa", 2, 24, 6, 1000, 4000, 64, 4.0, 5, [32, 64, 128, 256, 512]),
+                 ("c1_mha_256", 1, 4, 4, 256, 256, 64, 1.0, 1, [128])]
+        for name, Bc, Hqc, Hkvc, Sq, Sk, Dc, sq, ci, bks in cases:
+            fl = 4.0 * Bc * Hqc * Sq * Sk * Dc
+            cb = make_inputs(ts, Bc, Hqc, Hkvc, Sq, Sk, Dc, SEED0 + ci, sigma_q=sq, copies=1)
+            sc = ts.DeviceBuffer(ts.attn_flash_scratch_bytes(Dc, max(bks)))
+            res = {}
+            for bk in bks:
+                w, k = time_calls(ts, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, 0, bk, sc, 20, 3)
+                res["bk%d" % bk] = {"kernel_ms": k, "TFLOP_s": fl / (k * 1e-3) / 1e12,
+                                    "mfma_frac": fl / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+            res["parity"] = parity(ts, o, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, 0, 8, nthreads)
+            extra[name] = res
+            log(name, res)
+            for b in cb:
+                for x in b[:4]:
+                    x.free()
+            sc.free()
+
+    cpu = None if args.no_cpu else cpu_baseline(o, ts)
+    if cpu:
+        log("cpu baseline:", cpu)
+    line = {
+        "metric": "TFLOP/s & % bf16 MFMA peak, GQA 4k prefill; decode HBM GB/s",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, fp32 O)",
+        "config": {"workload": "c3 GQA prefill B4 Hq32 Hkv8 D128 Sq=Sk=4096 non-causal",
+                   "global_batch": B, "seq_len": S, "parallelism": "single GPU",
+                   "bk": args.bk, "input_copies": copies},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "kernel_ms": round(kern_ms, 4), "flop_per_launch": flops},
+        "cpu_baseline": cpu,
+        "parity": head_parity,
+        "device": info,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
