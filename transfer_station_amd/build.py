@@ -22,6 +22,8 @@ LIBNAME = "libattn_flash.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["attn_kernels.hip"]
+# Standalone roofline microbenchmark (MFMA peak, HBM copy/read), built next to the library.
+TOOL_SOURCES = {"roofline_bench": "roofline_bench.hip"}
 C_SOURCES = ["attn_flash.c", "attn_devutil.c", "attn_synth.c"]
 
 # Packed fp32 VALU forms are disabled for all device code on this platform.
@@ -46,6 +48,10 @@ def lib_path():
     return os.path.join(LIBDIR, LIBNAME)
 
 
+def tool_path(name):
+    return os.path.join(LIBDIR, name)
+
+
 def build(verbose=False, jobs=8):
     """Compile every source and link the shared library; returns its path."""
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
@@ -61,6 +67,9 @@ def build(verbose=False, jobs=8):
         o = os.path.join(OBJDIR, s + ".o")
         cmds.append(["gcc"] + CC_FLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
         objs.append(o)
+    for exe, src in TOOL_SOURCES.items():
+        cmds.append([hipcc] + HIPCC_FLAGS + [os.path.join(CSRC, src), "-o",
+                                             os.path.join(LIBDIR, exe)])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for out in ex.map(_run, cmds):
             if out and verbose:
