@@ -123,15 +123,14 @@ void *attn_flash_get_stream(void) { return t_stream; }
 
 /* ---- tile and split selection ------------------------------------------------------------ */
 /* Key-tile size of the prefill kernel for the caller's bk: the online-softmax update runs
- * once per KT keys. bk below 32 (one 32-key MFMA tile) runs at KT=32; bk above 128 is
- * processed as 128-key sub-blocks, each its own update (the result is bk-invariant within
- * the tolerance, as in the reference). */
-static int attn_kt_for_bk(int bk) {
-    if (bk <= 32)
-        return 32;
-    if (bk == 64)
-        return 64;
-    return 128;
+ * once per KT keys. bk below 32 (one 32-key MFMA tile) runs at KT=32; a bk above the largest
+ * tile that still fits two waves per SIMD (64 keys at D<=128 > 64, 128 keys at D<=64) is
+ * processed as sub-blocks of that size, each its own update (the result is bk-invariant
+ * within the tolerance, as in the reference). */
+static int attn_kt_for_bk(int bk, int dp) {
+    const int kt_max = (dp == 128) ? 64 : 128; /* largest tile that keeps 2 waves per SIMD */
+    int kt = (bk <= 32) ? 32 : (bk == 64 ? 64 : 128);
+    return kt < kt_max ? kt : kt_max;
 }
 
 #define ATTN_DECODE_ROWS 16 /* query rows per kv head the decode MFMA tile holds */
@@ -212,7 +211,7 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
                            who);
     } else {
         attn_hip_check(attn_hip_launch_prefill(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal ? 1 : 0,
-                                               vec, dp, attn_kt_for_bk(bk), c, st),
+                                               vec, dp, attn_kt_for_bk(bk, dp), c, st),
                        who);
     }
     if (tm) {

@@ -18,6 +18,7 @@
 //   attn_pack_v_kernel                     V [Hkv][Sk][D] -> V^T [Hkv][D][Sk]
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -283,6 +284,227 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
+// Prefill, fast path: D == DP (64 or 128) and 16-byte aligned tensors. Same tiling as
+// attn_prefill_kernel, plus:
+//   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
+//     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
+//     offset (the range-checked one); the scalar offset is always 0.
+//   * lazy rescale: the running max a row subtracts is only raised when a new score exceeds it
+//     by more than kLazyLog2 (in log2 units); p is then at most 2^kLazyLog2 and the accumulator
+//     rescale (alpha != 1) runs only on those rare tiles, decided wave-uniformly. In exact
+//     arithmetic the result is identical (softmax is shift-invariant and alpha == 1 otherwise).
+// ------------------------------------------------------------------------------------------
+constexpr float kLazyLog2 = 8.0f;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+template <int DP, int KT, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+    const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk,
+    float c, int nqt) {
+    static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
+    constexpr int D = DP;
+    constexpr int NT = NW * 64; // threads per workgroup
+    constexpr int BQ = NW * 32; // query rows per workgroup
+    constexpr int KSTR = DP + 8;
+    // V rows are 2*VSTR bytes apart; 2*VSTR = 64 (mod 256) puts the two 16-lane groups of a
+    // transposed read (same 4 rows, columns 32 bytes apart) on disjoint LDS banks.
+    // (The D=64, 128-key tile keeps a 32-byte pad so two workgroups still fit a CU's LDS.)
+    constexpr int VSTR = (DP == 64 && KT == 128) ? DP + 16 : DP + 32;
+    constexpr int NCH = KT * DP / 8 / NT;
+    static_assert(NCH >= 1 && (KT * DP / 8) % NT == 0, "chunking");
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * VSTR];
+
+    const int g = Hq / Hkv;
+    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int u = L / (g * nqt);
+    const int rr = L - u * (g * nqt);
+    const int qt = rr / g;
+    const int h = u * g + (rr - qt * g);
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int q0 = qt * BQ + w * 32;
+    const int myq = q0 + l32;
+
+    const uint16_t *Qh = Q + (size_t)h * Sq * D;
+    const uint32_t kvbytes = (uint32_t)Sk * D * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + (size_t)u * Sk * D, kvbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V + (size_t)u * Sk * D, kvbytes);
+
+    bf16x8 qb[DP / 16];
+#pragma unroll
+    for (int kk = 0; kk < DP / 16; ++kk)
+        qb[kk] = as_bf16x8(load_row8<true>(Qh, (size_t)myq, kk * 16 + hi * 8, D, myq < Sq));
+    // Q must be resident before the loop: otherwise the compiler's wait at the loop's first
+    // MFMA also waits for the next tile's prefetch (its count cannot tell the two apart).
+    // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+
+    int nkt = (Sk + KT - 1) / KT;
+    int wave_maxkey = (q0 < Sq) ? Sk - 1 : -1;
+    if (CAUSAL) {
+        const int last_row = min(qt * BQ + BQ - 1, Sq - 1);
+        const int maxkey = Sk - Sq + last_row;
+        nkt = (maxkey < 0) ? 0 : min(nkt, maxkey / KT + 1);
+        if (q0 < Sq)
+            wave_maxkey = min(Sk - 1, Sk - Sq + min(q0 + 31, Sq - 1));
+    }
+    const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + myq) : Sk - 1;
+    const float lazy_raw = kLazyLog2 / c; // headroom in raw-score units
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x16 o[DP / 32];
+#pragma unroll
+    for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            o[db][i] = 0.f;
+
+    // Tile kt's chunk r of this thread sits at byte kt*KT*D*2 + r*NT*16 + tid*16 of the head.
+    const uint32_t voff = (uint32_t)tid * 16u;
+    u32x4 kr[NCH], vr[NCH];
+    auto gload = [&](int kt) {
+        const uint32_t base = (uint32_t)kt * KT * D * 2 + voff;
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            kr[r] = buf_load16(rk, base + r * (NT * 16u), 0u);
+            vr[r] = buf_load16(rv, base + r * (NT * 16u), 0u);
+        }
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            const int cidx = tid + NT * r;
+            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+            *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
+            *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+        }
+    };
+
+    const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int g16 = lane >> 4, i16 = lane & 15;
+
+    if (nkt > 0) {
+        gload(0);
+        swrite(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nkt)
+            gload(kt + 1);
+        const int kbase = kt * KT;
+        if (kbase <= wave_maxkey) {
+            f32x16 s[KT / 32];
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    s[t][i] = 0.f;
+                // All K fragments of this 32-key sub-tile are read as one group ahead of its
+                // MFMA chain, so the LDS latency is paid once per sub-tile.
+                const uint16_t *kb = &Ks[buf][(t * 32 + kperm) * KSTR + hi * 8];
+                bf16x8 ka[DP / 16];
+#pragma unroll
+                for (int kk = 0; kk < DP / 16; ++kk)
+                    ka[kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb + kk * 16));
+#pragma unroll
+                for (int kk = 0; kk < DP / 16; ++kk)
+                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk], qb[kk], s[t], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0); // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, DP / 16, 0); // MFMAs
+            }
+            if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + q0)) {
+#pragma unroll
+                for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key = kbase + t * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
+                        if (key > lim)
+                            s[t][i] = kNegInf;
+                    }
+            }
+            float mx = kNegInf;
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    mx = fmaxf(mx, s[t][i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            // Raise the subtracted max only past the headroom (or from -inf), wave-uniformly.
+            const bool raise = mx > m_run + lazy_raw;
+            if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+                const float mnew = raise ? mx : m_run;
+                const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < DP / 32; ++db)
+                    o[db] *= alpha;
+                m_run = mnew;
+            }
+            const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
+            bf16x8 pk[KT / 16];
+            float ps[KT / 16];
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float p[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        p[j] = fast_exp2(fmaf(s[t][8 * hh + j], c, -mc));
+                        pk[2 * t + hh][j] = (__bf16)p[j];
+                    }
+                    ps[2 * t + hh] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                }
+            float psum = 0.f;
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j)
+                psum += ps[j];
+            l_run += psum;
+#pragma unroll
+            for (int cc = 0; cc < KT / 16; ++cc) {
+                const uint16_t *vb =
+                    &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR + (g16 & 1) * 16 + 4 * (i16 & 3)];
+#pragma unroll
+                for (int db = 0; db < DP / 32; ++db) {
+                    const bf16x8 a = join_tr(lds_read_tr(vb + db * 32), lds_read_tr(vb + db * 32 + 4 * VSTR));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < nkt)
+            swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
+    if (myq < Sq) {
+        float *orow = O + ((size_t)h * Sq + myq) * D;
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int d = db * 32 + i4 * 8 + 4 * hi;
+                f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
+                           o[db][4 * i4 + 3] * inv};
+                *reinterpret_cast<f32x4 *>(orow + d) = v;
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Decode (split-K). One workgroup per (kv head u, split sp) serves all M = g*Sq <= 16 query
 // rows of that kv head from ONE read of its K/V range [sp*kps, min(sp*kps+kps, Sk)). Waves
 // take interleaved 32-key tiles; per tile (v_mfma_f32_16x16x32_bf16):
@@ -506,10 +728,46 @@ hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t
     return hipGetLastError();
 }
 
+template <int DP, int KT, int NW, bool CAUSAL>
+hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                  float *O, int Hq, int Hkv, int Sq, int Sk, float c,
+                                  hipStream_t st) {
+    const int nqt = (Sq + NW * 32 - 1) / (NW * 32);
+    const long nblk = (long)Hq * nqt;
+    if (nblk <= 0 || nblk > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL>), dim3((unsigned)nblk),
+                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, c, nqt);
+    return hipGetLastError();
+}
+
+// Waves per workgroup for the fast prefill kernel: 8 (256 query rows, one workgroup per CU,
+// two waves per SIMD) unless ATTN_PREFILL_WAVES=4 selects 4 for tuning sweeps.
+static int prefill_waves() {
+    static int nw = -1;
+    if (nw < 0) {
+        const char *e = getenv("ATTN_PREFILL_WAVES");
+        nw = (e && atoi(e) == 4) ? 4 : 8;
+    }
+    return nw;
+}
+
+template <int DP, int KT, bool CAUSAL>
+hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                                 int Hq, int Hkv, int Sq, int Sk, float c, hipStream_t st) {
+    if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
+        if (prefill_waves() == 8)
+            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+}
+
 template <int DP, int KT>
 hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                              int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, float c,
                              hipStream_t st) {
+    if (vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL)
+        return causal ? launch_prefill_fast_t<DP, KT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st)
+                      : launch_prefill_fast_t<DP, KT, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
     if (causal)
         return vec ? launch_prefill_t<DP, KT, true, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st)
                    : launch_prefill_t<DP, KT, true, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
@@ -527,7 +785,9 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
     case 64:
         return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
     case 128:
-        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+        if constexpr (DP <= 64)
+            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+        return hipErrorInvalidValue;
     default:
         return hipErrorInvalidValue;
     }

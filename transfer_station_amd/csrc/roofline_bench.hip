@@ -65,6 +65,22 @@ __global__ __launch_bounds__(256) void mfma16_peak(float *out, int iters) {
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// VALU issue rate: 8 independent chains of v_exp_f32 (transcendental) or v_fma_f32 per lane.
+template <bool EXP>
+__global__ __launch_bounds__(256) void valu_rate(float *out, int iters) {
+    float x[8];
+    for (int i = 0; i < 8; ++i)
+        x[i] = -1.0f - 1e-3f * (threadIdx.x + i);
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            x[i] = EXP ? __builtin_amdgcn_exp2f(x[i]) - 1.5f : fmaf(x[i], 0.999f, -0.5f);
+    float s = 0.f;
+    for (int i = 0; i < 8; ++i)
+        s += x[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 // dst[i] = src[i] for i < n4 (float4 elements), grid-stride.
 __global__ __launch_bounds__(256) void hbm_copy(const f32x4 *__restrict__ src,
                                                 f32x4 *__restrict__ dst, size_t n4) {
@@ -119,6 +135,37 @@ static double run_mfma(int which) {
     return best;
 }
 
+// Wave-instructions per clock per SIMD for v_exp_f32 (EXP) or v_fma_f32.
+static double run_valu(bool exp) {
+    int cus = 0, clk_khz = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    CHECK(hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeClockRate, 0));
+    const int blocks = cus * 8, threads = 256, iters = 20000;
+    float *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        if (exp)
+            hipLaunchKernelGGL(valu_rate<true>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+        else
+            hipLaunchKernelGGL(valu_rate<false>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        // per chain step: one v_exp + one v_add (EXP) or one v_fma; count the op of interest
+        double wave_insts = (double)blocks * (threads / 64) * iters * 8;
+        double per_simd_clk = wave_insts / (cus * 4.0) / (ms * 1e-3 * clk_khz * 1e3);
+        if (per_simd_clk > best)
+            best = per_simd_clk;
+    }
+    CHECK(hipFree(out));
+    return best;
+}
+
 static double run_stream(int copy, size_t mib, int reps) {
     size_t bytes = mib << 20, n4 = bytes / 16;
     f32x4 *src, *dst;
@@ -161,6 +208,9 @@ int main(int argc, char **argv) {
     if (!strcmp(mode, "mfma")) {
         printf("{\"mfma32x32x16_bf16_tflops\": %.1f, \"mfma16x16x32_bf16_tflops\": %.1f}\n",
                run_mfma(32), run_mfma(16));
+    } else if (!strcmp(mode, "valu")) {
+        printf("{\"exp_chain_steps_per_simd_clk\": %.4f, \"fma_per_simd_clk\": %.4f}\n",
+               run_valu(true), run_valu(false));
     } else if (!strcmp(mode, "copy")) {
         printf("{\"copy_mib\": %zu, \"copy_gbps\": %.1f}\n", mib, run_stream(1, mib, 1));
     } else if (!strcmp(mode, "read")) {
