@@ -91,6 +91,24 @@ def traffic_from_profiles(name):
     return None
 
 
+def measured_peaks():
+    """Run the roofline microbenchmark (MFMA with constant and with random operands, HBM
+    stream read); returns its JSON fields or {} if the tool is not built."""
+    import subprocess
+    from transfer_station_amd import build as b
+    tool = b.tool_path("roofline_bench")
+    out = {}
+    for mode in ("mfma", "read"):
+        try:
+            r = subprocess.run([tool, mode, "2048"] if mode == "read" else [tool, mode],
+                               capture_output=True, text=True, timeout=120)
+            if r.returncode == 0:
+                out.update(json.loads(r.stdout.strip().splitlines()[-1]))
+        except (OSError, subprocess.SubprocessError, ValueError):
+            pass
+    return out
+
+
 def cpu_baseline(o, ts, budget_s=12.0):
     """The oracle on the headline workload's rows, 1 thread and all (<=16) threads."""
     B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
@@ -179,7 +197,9 @@ def main():
         extra["c2_gqa_decode"] = {"kernel_us": k * 1e3, "wall_us": w * 1e3,
                                   "GB_s": dbytes / (k * 1e-3) / 1e9,
                                   "hbm_frac": dbytes / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-                                  "bytes_per_call": dbytes, "parity": p2}
+                                  "bytes_per_call": dbytes, "parity": p2,
+                                  "traffic": traffic_from_profiles(
+                                      "attn_decode_c2_traffic.txt")}
         log("c2 decode:", extra["c2_gqa_decode"])
         for b in db:
             for x in b[:4]:
@@ -207,6 +227,8 @@ def main():
                     x.free()
             sc.free()
 
+    peaks = measured_peaks()
+    log("measured peaks:", peaks)
     cpu = None if args.no_cpu else cpu_baseline(o, ts)
     if cpu:
         log("cpu baseline:", cpu)
@@ -229,7 +251,11 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
-                     "kernel_ms": round(kern_ms, 4), "flop_per_launch": flops},
+                     "kernel_ms": round(kern_ms, 4), "flop_per_launch": flops,
+                     "measured_peaks": peaks,
+                     "frac_of_measured_random_operand_peak":
+                         (round(achieved / peaks["mfma32x32x16_bf16_random_operands_tflops"], 4)
+                          if peaks.get("mfma32x32x16_bf16_random_operands_tflops") else None)},
         "cpu_baseline": cpu,
         "parity": head_parity,
         "device": info,

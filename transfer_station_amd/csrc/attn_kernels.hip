@@ -80,6 +80,19 @@ __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t *p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(x[lane], x[lane ^ 32]) in the VALU: v_permlane32_swap exchanges the upper 32 lanes of its
+// first operand with the lower 32 lanes of its second, so with both operands holding x each lane
+// ends with its partner's value in one of the two; no LDS round trip (ds_bpermute) is involved.
+// The s_nop guards cover the VALU-write -> permlane-read and permlane-write -> VALU-read
+// hazards (measured: without the leading wait states the source is read stale). Written as
+// inline asm because the compiler's folding of the builtin drops the exchange when both
+// operands are the same value.
+__device__ __forceinline__ float max_xor32(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 2\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 2" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+
 __device__ __forceinline__ void lds_wave_fence() {
     // Wave-private LDS reuse: finish this wave's outstanding LDS traffic and keep the compiler
     // from moving LDS accesses across this point.
@@ -434,14 +447,21 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                             s[t][i] = kNegInf;
                     }
             }
-            float mx = kNegInf;
+            // Row max of the tile as a shallow tree (independent max3 leaves, then a combine),
+            // the partner half-row through the VALU exchange, then the wave-uniform lazy-rescale
+            // test; the exponentials and the P.V MFMAs follow in one branch-free block.
+            float mt[KT / 32][4];
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t)
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    mx = fmaxf(mx, s[t][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            // Raise the subtracted max only past the headroom (or from -inf), wave-uniformly.
+                for (int q = 0; q < 4; ++q)
+                    mt[t][q] = fmaxf(fmaxf(s[t][4 * q], s[t][4 * q + 1]),
+                                     fmaxf(s[t][4 * q + 2], s[t][4 * q + 3]));
+            float mx = kNegInf;
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+                mx = fmaxf(mx, fmaxf(fmaxf(mt[t][0], mt[t][1]), fmaxf(mt[t][2], mt[t][3])));
+            mx = max_xor32(mx);
             const bool raise = mx > m_run + lazy_raw;
             if (__builtin_amdgcn_ballot_w64(raise) != 0) {
                 const float mnew = raise ? mx : m_run;

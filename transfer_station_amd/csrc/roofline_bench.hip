@@ -46,6 +46,130 @@ __global__ __launch_bounds__(256) void mfma32_peak(float *out, int iters) {
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Same chains as mfma32_peak but with random bf16 operands that change every step (operand
+// bits toggle as in a real attention tile; constant operands draw less power and can clock
+// higher). r holds 64 random u32 per lane-slot, read from registers after one load.
+__global__ __launch_bounds__(256) void mfma32_peak_random(const unsigned *r, float *out, int iters) {
+    typedef __attribute__((ext_vector_type(4))) unsigned u4;
+    // eight random operand registers per lane, cycled so that consecutive MFMAs see different
+    // bits (as a real attention tile does); no VALU work in the loop
+    bf16x8 op[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        u4 v = *(const u4 *)(r + ((threadIdx.x & 63) * 8 + k) * 4);
+        v = (v & 0x80FF80FFu) | 0x3E003E00u; // bounded exponents, random sign and mantissa
+        op[k] = __builtin_bit_cast(bf16x8, v);
+    }
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[k], op[k + 1], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[k + 1], op[(k + 2) & 7], c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[(k + 3) & 7], op[k], c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[(k + 5) & 7], op[(k + 6) & 7], c3, 0, 0, 0);
+        }
+    }
+    float s = 0.f;
+    for (int i = 0; i < 16; ++i)
+        s += c0[i] + c1[i] + c2[i] + c3[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// One or two dependent accumulation chains per wave (how a single S^T chain is served).
+template <int CH>
+__global__ __launch_bounds__(256) void mfma32_chain(float *out, int iters) {
+    bf16x8 a, b;
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(float)((threadIdx.x + i) & 7);
+        b[i] = (__bf16)(float)((threadIdx.x * 3 + i) & 7);
+    }
+    f32x16 c[CH] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int ch = 0; ch < CH; ++ch)
+                c[ch] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c[ch], 0, 0, 0);
+    float s = 0.f;
+    for (int ch = 0; ch < CH; ++ch)
+        for (int i = 0; i < 16; ++i)
+            s += c[ch][i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// One wave per SIMD: 2 MFMA chains plus NV independent VALU fma per MFMA, in program order.
+template <int NV>
+__global__ __launch_bounds__(256) void mfma_valu_coissue(float *out, int iters) {
+    bf16x8 a, b;
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(float)((threadIdx.x + i) & 7);
+        b[i] = (__bf16)(float)((threadIdx.x * 3 + i) & 7);
+    }
+    f32x16 c0 = {}, c1 = {};
+    float v[16];
+    for (int i = 0; i < 16; ++i)
+        v[i] = 1.0f + threadIdx.x * 1e-3f + i;
+    for (int it = 0; it < iters; ++it) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            v[k] = fmaf(v[k], 0.999f, 0.5f);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            v[8 + k % 8] = fmaf(v[8 + k % 8], 0.999f, 0.25f);
+        if constexpr (NV > 0) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+        }
+    }
+    float s = 0.f;
+    for (int i = 0; i < 16; ++i)
+        s += c0[i] + c1[i] + v[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// Two waves per SIMD: waves 0-3 issue only MFMA (2 chains), waves 4-7 only VALU fma
+// (NV per MFMA-equivalent step); measures how far a VALU wave slows an MFMA wave.
+template <int NV, bool AG>
+__global__ __launch_bounds__(512) void mfma_valu_split(float *out, int iters) {
+    const int w = threadIdx.x >> 6;
+    float s = 0.f;
+    if (w < 4) {
+        bf16x8 a, b;
+        for (int i = 0; i < 8; ++i) {
+            a[i] = (__bf16)(float)((threadIdx.x + i) & 7);
+            b[i] = (__bf16)(float)((threadIdx.x * 3 + i) & 7);
+        }
+        f32x16 c0 = {}, c1 = {};
+        for (int it = 0; it < iters; ++it) {
+            if (AG) { // accumulators pinned in AGPRs
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c0) : "v"(a), "v"(b));
+                asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c1) : "v"(a), "v"(b));
+            } else {
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
+            }
+        }
+        for (int i = 0; i < 16; ++i)
+            s += c0[i] + c1[i];
+    } else {
+        float v[8];
+        for (int i = 0; i < 8; ++i)
+            v[i] = 1.0f + threadIdx.x * 1e-3f + i;
+        for (int it = 0; it < iters; ++it)
+#pragma unroll
+            for (int k = 0; k < 2 * NV; ++k)
+                v[k % 8] = fmaf(v[k % 8], 0.999f, 0.5f);
+        for (int i = 0; i < 8; ++i)
+            s += v[i];
+    }
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 __global__ __launch_bounds__(256) void mfma16_peak(float *out, int iters) {
     bf16x8 a, b;
     for (int i = 0; i < 8; ++i) {
@@ -81,6 +205,38 @@ __global__ __launch_bounds__(256) void valu_rate(float *out, int iters) {
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// LDS read throughput: every lane reads 16 bytes (ds_read_b128) or 8 bytes transposed
+// (ds_read_b64_tr_b16) per step from a 64 KiB tile; addresses stay inside the tile.
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+template <bool TR>
+__global__ __launch_bounds__(256) void lds_rate(unsigned *out, int iters) {
+    __shared__ __attribute__((aligned(16))) unsigned short tile[32768];
+    for (int i = threadIdx.x; i < 32768; i += 256)
+        tile[i] = (unsigned short)i;
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    unsigned acc = 0;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            // 16 KiB window per wave, rows of 256 B plus a 16 B pad (bank-conflict free)
+            const int base = ((w * 8 + k) & 31) * 512 + ((it & 7) * 64);
+            if (TR) {
+                const int off = base + (lane & 15) * 136 / 4 * 4 + (lane >> 4) * 4;
+                s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_t *)(tile + (off & 32767 & ~3)));
+                acc ^= (unsigned)v[0] ^ ((unsigned)v[3] << 16);
+            } else {
+                const int off = base + (lane & 15) * 136 + (lane >> 4) * 8;
+                u32x4_t v = *(const u32x4_t *)(tile + (off & 32767 & ~7));
+                acc ^= v[0] ^ v[3];
+            }
+        }
+    }
+    out[blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}
+
 // dst[i] = src[i] for i < n4 (float4 elements), grid-stride.
 __global__ __launch_bounds__(256) void hbm_copy(const f32x4 *__restrict__ src,
                                                 f32x4 *__restrict__ dst, size_t n4) {
@@ -104,6 +260,41 @@ static double time_ms(hipEvent_t a, hipEvent_t b) {
     CHECK(hipEventSynchronize(b));
     CHECK(hipEventElapsedTime(&ms, a, b));
     return ms;
+}
+
+static double run_mfma_random() {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus * 8, threads = 256, iters = 5000;
+    float *out;
+    unsigned *r;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    CHECK(hipMalloc(&r, 64 * 8 * 4 * sizeof(unsigned)));
+    unsigned h[2048];
+    unsigned x = 0x12345678u;
+    for (int i = 0; i < 2048; ++i) {
+        x ^= x << 13; x ^= x >> 17; x ^= x << 5;
+        h[i] = x;
+    }
+    CHECK(hipMemcpy(r, h, sizeof h, hipMemcpyHostToDevice));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        hipLaunchKernelGGL(mfma32_peak_random, dim3(blocks), dim3(threads), 0, 0, r, out, iters);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        double flops = (double)blocks * (threads / 64) * iters * 16 * 32768.0;
+        double tf = flops / (ms * 1e-3) / 1e12;
+        if (tf > best)
+            best = tf;
+    }
+    CHECK(hipFree(out));
+    CHECK(hipFree(r));
+    return best;
 }
 
 static double run_mfma(int which) {
@@ -136,6 +327,99 @@ static double run_mfma(int which) {
 }
 
 // Wave-instructions per clock per SIMD for v_exp_f32 (EXP) or v_fma_f32.
+// TFLOP/s with CH dependent chains per wave, `wpb` waves per SIMD (blocks of 256 threads).
+static double run_chain(int ch, int waves_per_simd) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus * waves_per_simd, threads = 256, iters = 5000;
+    float *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        if (ch == 1)
+            hipLaunchKernelGGL(mfma32_chain<1>, dim3(blocks), dim3(threads), 0, 0, out, iters * 4);
+        else if (ch == 2)
+            hipLaunchKernelGGL(mfma32_chain<2>, dim3(blocks), dim3(threads), 0, 0, out, iters * 2);
+        else
+            hipLaunchKernelGGL(mfma32_chain<4>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        double flops = (double)blocks * 4 * iters * 16 * 32768.0;
+        double tf = flops / (ms * 1e-3) / 1e12;
+        if (tf > best)
+            best = tf;
+    }
+    CHECK(hipFree(out));
+    return best;
+}
+
+static double run_coissue(int nv) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus, threads = 256, iters = 20000; // one wave per SIMD
+    float *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        switch (nv) {
+        case 0: hipLaunchKernelGGL(mfma_valu_coissue<0>, dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        case 2: hipLaunchKernelGGL(mfma_valu_coissue<2>, dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        case 4: hipLaunchKernelGGL(mfma_valu_coissue<4>, dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        case 6: hipLaunchKernelGGL(mfma_valu_coissue<6>, dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        default: hipLaunchKernelGGL(mfma_valu_coissue<8>, dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        }
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        double flops = (double)blocks * 4 * iters * 2 * 32768.0;
+        double tf = flops / (ms * 1e-3) / 1e12;
+        if (tf > best)
+            best = tf;
+    }
+    CHECK(hipFree(out));
+    return best;
+}
+
+template <bool AG>
+static double run_split(int nv) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus, threads = 512, iters = 20000;
+    float *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        switch (nv) {
+        case 0: hipLaunchKernelGGL((mfma_valu_split<0, AG>), dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        case 4: hipLaunchKernelGGL((mfma_valu_split<4, AG>), dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        case 6: hipLaunchKernelGGL((mfma_valu_split<6, AG>), dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        default: hipLaunchKernelGGL((mfma_valu_split<8, AG>), dim3(blocks), dim3(threads), 0, 0, out, iters); break;
+        }
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        double flops = (double)blocks * 4 * iters * 2 * 32768.0;
+        double tf = flops / (ms * 1e-3) / 1e12;
+        if (tf > best)
+            best = tf;
+    }
+    CHECK(hipFree(out));
+    return best;
+}
+
 static double run_valu(bool exp) {
     int cus = 0, clk_khz = 0;
     CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
@@ -161,6 +445,36 @@ static double run_valu(bool exp) {
         double per_simd_clk = wave_insts / (cus * 4.0) / (ms * 1e-3 * clk_khz * 1e3);
         if (per_simd_clk > best)
             best = per_simd_clk;
+    }
+    CHECK(hipFree(out));
+    return best;
+}
+
+// Bytes per clock per CU delivered by LDS reads.
+static double run_lds(bool tr) {
+    int cus = 0, clk_khz = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    CHECK(hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeClockRate, 0));
+    const int blocks = cus * 2, threads = 256, iters = 4000;
+    unsigned *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(unsigned)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    double best = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        if (tr)
+            hipLaunchKernelGGL(lds_rate<true>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+        else
+            hipLaunchKernelGGL(lds_rate<false>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        double ms = time_ms(a, b);
+        double bytes = (double)blocks * threads * iters * 8 * (tr ? 8 : 16);
+        double bpc = bytes / cus / (ms * 1e-3 * clk_khz * 1e3);
+        if (bpc > best)
+            best = bpc;
     }
     CHECK(hipFree(out));
     return best;
@@ -206,8 +520,26 @@ int main(int argc, char **argv) {
         return 2;
     }
     if (!strcmp(mode, "mfma")) {
-        printf("{\"mfma32x32x16_bf16_tflops\": %.1f, \"mfma16x16x32_bf16_tflops\": %.1f}\n",
-               run_mfma(32), run_mfma(16));
+        printf("{\"mfma32x32x16_bf16_tflops\": %.1f, \"mfma16x16x32_bf16_tflops\": %.1f, "
+               "\"mfma32x32x16_bf16_random_operands_tflops\": %.1f}\n",
+               run_mfma(32), run_mfma(16), run_mfma_random());
+    } else if (!strcmp(mode, "split")) {
+        for (int nv = 0; nv <= 8; nv += (nv == 0 ? 4 : 2))
+            printf("{\"valu_per_mfma_other_wave\": %d, \"mfma_tflops_vgpr_acc\": %.1f, "
+                   "\"mfma_tflops_agpr_acc\": %.1f}\n",
+                   nv, run_split<false>(nv), run_split<true>(nv));
+    } else if (!strcmp(mode, "coissue")) {
+        for (int nv = 0; nv <= 8; nv += 2)
+            printf("{\"valu_per_mfma\": %d, \"one_wave_per_simd_mfma_tflops\": %.1f}\n", nv,
+                   run_coissue(nv));
+    } else if (!strcmp(mode, "chain")) {
+        for (int w = 1; w <= 2; ++w)
+            printf("{\"waves_per_simd\": %d, \"chain1_tflops\": %.1f, \"chain2_tflops\": %.1f, "
+                   "\"chain4_tflops\": %.1f}\n",
+                   w, run_chain(1, w), run_chain(2, w), run_chain(4, w));
+    } else if (!strcmp(mode, "lds")) {
+        printf("{\"lds_read_b128_bytes_per_clk_cu\": %.1f, \"lds_read_tr_b64_bytes_per_clk_cu\": %.1f}\n",
+               run_lds(false), run_lds(true));
     } else if (!strcmp(mode, "valu")) {
         printf("{\"exp_chain_steps_per_simd_clk\": %.4f, \"fma_per_simd_clk\": %.4f}\n",
                run_valu(true), run_valu(false));
@@ -216,11 +548,12 @@ int main(int argc, char **argv) {
     } else if (!strcmp(mode, "read")) {
         printf("{\"read_mib\": %zu, \"read_gbps\": %.1f}\n", mib, run_stream(0, mib, 5));
     } else if (!strcmp(mode, "all")) {
-        double m32 = run_mfma(32), m16 = run_mfma(16);
+        double m32 = run_mfma(32), m16 = run_mfma(16), mr = run_mfma_random();
         double cp = run_stream(1, mib, 5), rd = run_stream(0, mib, 5);
         printf("{\"mfma32x32x16_bf16_tflops\": %.1f, \"mfma16x16x32_bf16_tflops\": %.1f, "
+               "\"mfma32x32x16_bf16_random_operands_tflops\": %.1f, "
                "\"copy_gbps\": %.1f, \"read_gbps\": %.1f, \"stream_mib\": %zu}\n",
-               m32, m16, cp, rd, mib);
+               m32, m16, mr, cp, rd, mib);
     } else {
         fprintf(stderr, "usage: %s [all|mfma|copy MiB|read MiB]\n", argv[0]);
         return 2;
