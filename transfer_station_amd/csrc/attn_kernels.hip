@@ -341,8 +341,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int u = L / (g * nqt);
     const int rr = L - u * (g * nqt);
-    const int qt = rr / g;
-    const int h = u * g + (rr - qt * g);
+    // Causal work grows with the query tile, so within a kv head the last (heaviest) tiles are
+    // dispatched first: longest-first keeps the tail of the grid short.
+    const int qt = CAUSAL ? nqt - 1 - rr / g : rr / g;
+    const int h = u * g + (rr - (rr / g) * g);
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hi = lane >> 5;
