@@ -233,6 +233,58 @@ def test_pack_v_full_transposes_exactly():
     assert np.array_equal(got, V.reshape(Hkv, Sk, D).transpose(0, 2, 1))
 
 
+# ---- v_prepacked = 1: V^T [Hkv][D][Sk] input (flash.c:751-753,770,812-833) -----------------------
+# The reference changes only V's stride when V is pre-packed, so the math is identical. Here the
+# V^T operand of the P.V MFMA holds the same values in the same positions either way, so O is
+# bit-identical whenever both layouts run the same kernel. They do not when D is 64 or 128 and
+# Sk % 8 != 0 (a V^T row is then not 16-byte aligned and the prefill takes the general kernel):
+# those cases are held to the oracle tolerance only.
+VT_CASES = [
+    # name, Hq, Hkv, Sq, Sk, D, causal, bk
+    ("fast D128 partial tile", 8, 2, 300, 1000, 128, 0, 128),
+    ("fast D128 causal", 8, 2, 513, 1024, 128, 1, 64),
+    ("fast D64 kt128 causal", 4, 4, 257, 520, 64, 1, 256),
+    ("fast D64 kt32 Sk<KT", 4, 2, 100, 24, 64, 0, 16),
+    ("general D40 causal", 6, 3, 130, 70, 40, 1, 128),
+    ("general D128 Sk%8!=0", 8, 2, 200, 333, 128, 0, 128),
+    ("general D64 Sk%8!=0 causal", 4, 1, 64, 77, 64, 1, 32),
+    ("general D7", 4, 2, 40, 50, 7, 0, 64),
+    ("decode Sq=1 split", 8, 2, 1, 2048, 128, 0, 128),
+    ("decode Sq=2 causal", 4, 1, 2, 1000, 64, 1, 128),
+    ("decode Sk%8!=0", 8, 1, 2, 4099, 128, 1, 128),
+    ("decode D40", 4, 2, 1, 300, 40, 0, 128),
+]
+
+
+@pytest.mark.parametrize("case", VT_CASES, ids=[c[0] for c in VT_CASES])
+def test_v_prepacked(oracle, case):
+    name, Hq, Hkv, Sq, Sk, D, causal, bk = case
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 40 + Sk)
+    base = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+    packed = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, prepack_v=True)
+    vt_host = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
+    direct = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=1)
+    assert np.array_equal(packed.view(np.uint32), direct.view(np.uint32))
+    decode = (Hq // Hkv) * Sq <= 16
+    same_kernel = decode or D not in (64, 128) or Sk % 8 == 0
+    if same_kernel:
+        nd = int(np.count_nonzero(packed.view(np.uint32) != base.view(np.uint32)))
+        say("   v_prepacked vs row-major: %d differing outputs" % nd)
+        assert nd == 0
+    check(oracle, "v_prepacked " + name, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, O=packed)
+
+
+def test_v_prepacked_c3_4k(oracle):
+    """The headline shape with a pre-packed V: bit-identical to the row-major run."""
+    B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
+    Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, S, S, D, SEED0 + 3)
+    base = ts.run_attention(Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128)
+    packed = ts.run_attention(Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128, prepack_v=True)
+    assert np.array_equal(packed.view(np.uint32), base.view(np.uint32))
+    check(oracle, "v_prepacked c3 4k", Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128, ref_cap=8,
+          O=packed)
+
+
 def test_timing_struct_and_scratch_reuse(oracle):
     Hq, Hkv, Sq, Sk, D = 8, 2, 1, 2048, 128
     bk_max = 4096

@@ -183,12 +183,25 @@ def synth_lcg_qkv(Hq, Hkv, Sq, Sk, D, seed=0x12345678):
     return tuple(arrs)
 
 
-def run_attention(Qh, Kh, Vh, Hq, Hkv, Sq, Sk, D, causal, bk=ATTN_BK_DEFAULT, v_prepacked=0):
-    """Host arrays in, host O out: uploads, runs attn_flash once, downloads."""
+def run_attention(Qh, Kh, Vh, Hq, Hkv, Sq, Sk, D, causal, bk=ATTN_BK_DEFAULT, v_prepacked=0,
+                  prepack_v=False):
+    """Host arrays in, host O out: uploads, runs attn_flash once, downloads.
+
+    v_prepacked=1: Vh is already V^T [Hkv][D][Sk]. prepack_v=True: Vh is row-major V; it is
+    transposed on the device by pack_v_full into a second buffer and attn_flash runs with
+    v_prepacked=1 (the reference's --prepack-v flow, flash.c:1074-1082)."""
+    if prepack_v and v_prepacked:
+        raise ValueError("prepack_v packs a row-major V; do not combine it with v_prepacked=1")
     with DeviceBuffer.from_array(Qh) as dq, DeviceBuffer.from_array(Kh) as dk, \
             DeviceBuffer.from_array(Vh) as dv, DeviceBuffer(Hq * Sq * D * 4) as do, \
-            DeviceBuffer(attn_flash_scratch_bytes(D, bk)) as ds:
+            DeviceBuffer(attn_flash_scratch_bytes(D, bk)) as ds, \
+            DeviceBuffer(dv.nbytes if prepack_v else 1) as dvp:
         do.fill_bytes(0xFF)  # NaN poison: every row must be written
-        attn_flash(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, causal, bk, ds, v_prepacked)
+        if prepack_v:
+            dvp.fill_bytes(0xFF)
+            pack_v_full(dv, dvp, Hkv, Sk, D)
+            attn_flash(dq, dk, dvp, do, Hq, Hkv, Sq, Sk, D, causal, bk, ds, 1)
+        else:
+            attn_flash(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, causal, bk, ds, v_prepacked)
         synchronize()
         return do.download(np.float32, Hq * Sq * D)

@@ -17,12 +17,12 @@
 
 /* HIP launchers (attn_kernels.hip). Each returns a hipError_t. */
 int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                            int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int dp,
-                            int kt, float c, void *stream);
+                            int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
+                            int dp, int kt, float c, void *stream);
 int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
-                           int D, int causal, int vec, int dp, float c, int nsplit, int kps,
-                           void *stream);
+                           int D, int causal, int vec, int vt, int dp, float c, int nsplit,
+                           int kps, void *stream);
 int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, float *O, int rows,
                           int D, int nsplit, float c, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
@@ -183,15 +183,16 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         attn_fail(who, "Q, K, V and O must be device pointers");
     if (!scratch || ((uintptr_t)scratch % ATTN_SCRATCH_ALIGN) != 0)
         attn_fail(who, "scratch must be non-NULL and ATTN_SCRATCH_ALIGN-aligned");
-    if (v_prepacked)
-        attn_fail(who, "v_prepacked=1 (V^T input) is not supported by this build yet");
 
     void *st = t_stream;
     const int group = Hq / Hkv;
     const float scale = 1.0f / sqrtf((float)D);
     const float c = scale * 1.44269504088896341f;
     const int dp = attn_dp_for_d(D);
-    const int vec = (D % 8 == 0) &&
+    /* v_prepacked (flash.c:751-753,770): V is V^T [Hkv][D][Sk], rows of stride Sk. 16-byte
+     * vector loads then also need Sk % 8 == 0 (each d row starting 16-byte aligned). */
+    const int vt = v_prepacked ? 1 : 0;
+    const int vec = (D % 8 == 0) && (!vt || Sk % 8 == 0) &&
                     ((((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15u) == 0);
 
     if (tm) {
@@ -204,14 +205,14 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         struct attn_carve cv;
         attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_decode(Q, K, V, O, cv.m, cv.l, cv.acc, Hq, Hkv, Sq, Sk, D,
-                                              causal ? 1 : 0, vec, dp, c, nsplit, kps, st),
+                                              causal ? 1 : 0, vec, vt, dp, c, nsplit, kps, st),
                        who);
         if (nsplit > 1)
             attn_hip_check(attn_hip_launch_merge(cv.m, cv.l, cv.acc, O, Hq * Sq, D, nsplit, c, st),
                            who);
     } else {
         attn_hip_check(attn_hip_launch_prefill(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal ? 1 : 0,
-                                               vec, dp, attn_kt_for_bk(bk, dp), c, st),
+                                               vec, vt, dp, attn_kt_for_bk(bk, dp), c, st),
                        who);
     }
     if (tm) {

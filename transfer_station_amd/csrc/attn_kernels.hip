@@ -12,13 +12,18 @@
 // products s, p = 2^(s*c - m*c) equals e^(scale*s - scale*m).
 //
 // Kernels:
-//   attn_prefill_kernel<DP,KT,CAUSAL,VEC>  MFMA prefill; one workgroup = 4 waves x 32 query rows
-//   attn_decode_kernel<DP,CAUSAL,VEC>      split-K decode for g*Sq <= 16 rows per kv head
+//   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D == DP in {64, 128}; one
+//                                          workgroup = NW waves x 32 query rows
+//   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 128 and alignment
+//   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 16 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
 //   attn_pack_v_kernel                     V [Hkv][Sk][D] -> V^T [Hkv][D][Sk]
+// VT selects a pre-transposed V ([Hkv][D][Sk], pack_v_full's layout).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 namespace {
 
@@ -59,6 +64,25 @@ __device__ __forceinline__ u32x4 load_row8(const uint16_t *base, size_t row, int
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         e[j] = (col + j < D) ? (uint32_t)p[j] : 0u;
+    u32x4 r = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+    return r;
+}
+
+// Eight consecutive keys [key, key+8) of row d of a V^T head ([D][Sk], row stride Sk), zero-filled
+// at d >= D or key >= klim. VEC requires Sk % 8 == 0 (with key % 8 == 0 and klim % 8 == 0 a chunk
+// is then wholly inside or wholly outside) and a 16-byte aligned base.
+template <bool VEC>
+__device__ __forceinline__ u32x4 load_vt8(const uint16_t *base, int d, int key, int Sk, int D,
+                                          int klim) {
+    if (d >= D || key >= klim)
+        return zero4();
+    const uint16_t *p = base + (size_t)d * Sk + key;
+    if (VEC)
+        return *reinterpret_cast<const u32x4 *>(p);
+    uint32_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        e[j] = (key + j < klim) ? (uint32_t)p[j] : 0u;
     u32x4 r = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
     return r;
 }
@@ -109,8 +133,11 @@ __device__ __forceinline__ void lds_wave_fence() {
 //                                    B = P^T straight from the S^T registers)
 // The S^T operand rows are permuted (bits 2 and 3 of the row swapped within each 16-row half)
 // so that a lane's 8 P values for one 16-key MFMA step are 8 consecutive keys.
+// VT: V arrives pre-transposed ([Hkv][D][Sk], pack_v_full's output). The tile is then staged
+// d-major (DP rows of KT keys), and the V^T operand of the P.V MFMA is a plain 16-byte LDS read
+// of 8 consecutive keys of one d row; the operand values, and so the result, are the same.
 // ------------------------------------------------------------------------------------------
-template <int DP, int KT, bool CAUSAL, bool VEC>
+template <int DP, int KT, bool CAUSAL, bool VEC, bool VT>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
@@ -118,10 +145,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int KSTR = DP + 8;  // LDS row stride (elements) of K: 16-byte pad
     constexpr int VSTR = DP + 16; // LDS row stride of V: 32-byte pad
+    constexpr int VTSTR = KT + 8; // LDS row stride of a V^T tile (VT): 16-byte pad
     constexpr int NCH = KT * DP / 8 / 256; // 16-byte chunks per thread per tile, per tensor
     static_assert(NCH >= 1 && (KT * DP / 8) % 256 == 0, "chunking");
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * VSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][VT ? DP * VTSTR : KT * VSTR];
 
     const int g = Hq / Hkv;
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -173,7 +201,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
             const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
             const int key = kt * KT + row;
             kr[r] = load_row8<VEC>(Kh, (size_t)key, col, D, key < Sk);
-            vr[r] = load_row8<VEC>(Vh, (size_t)key, col, D, key < Sk);
+            if (VT) {
+                const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
+                vr[r] = load_vt8<VEC>(Vh, d, kt * KT + kc, Sk, D, Sk);
+            } else {
+                vr[r] = load_row8<VEC>(Vh, (size_t)key, col, D, key < Sk);
+            }
         }
     };
     auto swrite = [&](int buf) {
@@ -182,7 +215,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
             const int cidx = tid + 256 * r;
             const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
             *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
-            *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+            if (VT) {
+                const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
+                *reinterpret_cast<u32x4 *>(&Vs[buf][d * VTSTR + kc]) = vr[r];
+            } else {
+                *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+            }
         }
     };
 
@@ -257,12 +295,24 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
                     o[db][i] *= alpha;
 #pragma unroll
             for (int cc = 0; cc < KT / 16; ++cc) {
-                const uint16_t *vb =
-                    &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR + (g16 & 1) * 16 + 4 * (i16 & 3)];
+                if (VT) {
+                    // lane: d row 32db + l32, keys 16cc + 8hi .. +7 (the k index of pk[cc]).
+                    const uint16_t *vb = &Vs[buf][l32 * VTSTR + cc * 16 + 8 * hi];
 #pragma unroll
-                for (int db = 0; db < DP / 32; ++db) {
-                    const bf16x8 a = join_tr(lds_read_tr(vb + db * 32), lds_read_tr(vb + db * 32 + 4 * VSTR));
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    for (int db = 0; db < DP / 32; ++db) {
+                        const bf16x8 a =
+                            as_bf16x8(*reinterpret_cast<const u32x4 *>(vb + db * 32 * VTSTR));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    }
+                } else {
+                    const uint16_t *vb = &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR +
+                                                  (g16 & 1) * 16 + 4 * (i16 & 3)];
+#pragma unroll
+                    for (int db = 0; db < DP / 32; ++db) {
+                        const bf16x8 a = join_tr(lds_read_tr(vb + db * 32),
+                                                 lds_read_tr(vb + db * 32 + 4 * VSTR));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -318,7 +368,7 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-template <int DP, int KT, int NW, bool CAUSAL>
+template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk,
@@ -332,10 +382,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     // transposed read (same 4 rows, columns 32 bytes apart) on disjoint LDS banks.
     // (The D=64, 128-key tile keeps a 32-byte pad so two workgroups still fit a CU's LDS.)
     constexpr int VSTR = (DP == 64 && KT == 128) ? DP + 16 : DP + 32;
+    constexpr int VTSTR = KT + 8; // V^T tile (VT): DP rows of KT keys, 16-byte pad
     constexpr int NCH = KT * DP / 8 / NT;
     static_assert(NCH >= 1 && (KT * DP / 8) % NT == 0, "chunking");
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * VSTR];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][VT ? DP * VTSTR : KT * VSTR];
 
     const int g = Hq / Hkv;
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -386,6 +437,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
             o[db][i] = 0.f;
 
     // Tile kt's chunk r of this thread sits at byte kt*KT*D*2 + r*NT*16 + tid*16 of the head.
+    // A V^T chunk (VT) is keys [kt*KT + kc, +8) of row d: byte (d*Sk + kt*KT + kc)*2, which
+    // needs Sk % 8 == 0; a chunk past Sk would wrap into row d+1, so it gets an offset beyond
+    // the buffer's range (kvbytes < 2^31) and reads as zero.
     const uint32_t voff = (uint32_t)tid * 16u;
     u32x4 kr[NCH], vr[NCH];
     auto gload = [&](int kt) {
@@ -393,7 +447,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 #pragma unroll
         for (int r = 0; r < NCH; ++r) {
             kr[r] = buf_load16(rk, base + r * (NT * 16u), 0u);
-            vr[r] = buf_load16(rv, base + r * (NT * 16u), 0u);
+            if (VT) {
+                const int cidx = tid + NT * r;
+                const int d = cidx / (KT / 8), key = kt * KT + (cidx % (KT / 8)) * 8;
+                const uint32_t off = (key < Sk) ? ((uint32_t)d * Sk + key) * 2u : 0x80000000u;
+                vr[r] = buf_load16(rv, off, 0u);
+            } else {
+                vr[r] = buf_load16(rv, base + r * (NT * 16u), 0u);
+            }
         }
     };
     auto swrite = [&](int buf) {
@@ -402,7 +463,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
             const int cidx = tid + NT * r;
             const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
             *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
-            *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+            if (VT) {
+                const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
+                *reinterpret_cast<u32x4 *>(&Vs[buf][d * VTSTR + kc]) = vr[r];
+            } else {
+                *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
+            }
         }
     };
 
@@ -496,12 +562,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
             l_run += psum;
 #pragma unroll
             for (int cc = 0; cc < KT / 16; ++cc) {
-                const uint16_t *vb =
-                    &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR + (g16 & 1) * 16 + 4 * (i16 & 3)];
+                if (VT) {
+                    const uint16_t *vb = &Vs[buf][l32 * VTSTR + cc * 16 + 8 * hi];
 #pragma unroll
-                for (int db = 0; db < DP / 32; ++db) {
-                    const bf16x8 a = join_tr(lds_read_tr(vb + db * 32), lds_read_tr(vb + db * 32 + 4 * VSTR));
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    for (int db = 0; db < DP / 32; ++db) {
+                        const bf16x8 a =
+                            as_bf16x8(*reinterpret_cast<const u32x4 *>(vb + db * 32 * VTSTR));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    }
+                } else {
+                    const uint16_t *vb = &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR +
+                                                  (g16 & 1) * 16 + 4 * (i16 & 3)];
+#pragma unroll
+                    for (int db = 0; db < DP / 32; ++db) {
+                        const bf16x8 a = join_tr(lds_read_tr(vb + db * 32),
+                                                 lds_read_tr(vb + db * 32 + 4 * VSTR));
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -534,8 +611,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 //   O^T[d][row]  += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from a wave-private LDS tile)
 // The 4 waves merge in LDS; the workgroup writes O directly (nsplit == 1) or one partial
 // (m, l, acc[D]) per row into the caller's scratch for attn_merge_kernel.
+// VT: V arrives as V^T ([Hkv][D][Sk]); the V^T operand (row d, 8 consecutive keys per lane) is
+// then loaded from global memory straight into its register layout, like K, with no LDS tile.
 // ------------------------------------------------------------------------------------------
-template <int DP, bool CAUSAL, bool VEC>
+template <int DP, bool CAUSAL, bool VEC, bool VT>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
@@ -584,19 +663,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             for (int kk = 0; kk < DP / 32; ++kk)
                 ka[t][kk] = load_row8<VEC>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
         }
-        u32x4 vv[VNCH];
+        u32x4 vv[VT ? DP / 16 : VNCH];
+        if (VT) {
+            // lane: d row 16db + r16, keys tb + 8grp .. +7 (the k index of pk below).
 #pragma unroll
-        for (int r = 0; r < VNCH; ++r) {
-            const int cidx = lane + 64 * r;
-            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-            vv[r] = load_row8<VEC>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
-        }
-        lds_wave_fence(); // previous tile's transposed reads are complete
+            for (int db = 0; db < DP / 16; ++db)
+                vv[db] = load_vt8<VEC>(Vh, db * 16 + r16, tb + 8 * grp, Sk, D, k1);
+        } else {
 #pragma unroll
-        for (int r = 0; r < VNCH; ++r) {
-            const int cidx = lane + 64 * r;
-            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-            *reinterpret_cast<u32x4 *>(&vt[row * VSTR + col]) = vv[r];
+            for (int r = 0; r < VNCH; ++r) {
+                const int cidx = lane + 64 * r;
+                const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+                vv[r] = load_row8<VEC>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
+            }
+            lds_wave_fence(); // previous tile's transposed reads are complete
+#pragma unroll
+            for (int r = 0; r < VNCH; ++r) {
+                const int cidx = lane + 64 * r;
+                const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
+                *reinterpret_cast<u32x4 *>(&vt[row * VSTR + col]) = vv[r];
+            }
         }
         f32x4 s[2];
 #pragma unroll
@@ -639,12 +725,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
         for (int db = 0; db < DP / 16; ++db)
             o[db] *= alpha;
-        lds_wave_fence(); // this tile's V is in LDS before the transposed reads
-        const uint16_t *vb = &vt[(8 * grp + (r16 >> 2)) * VSTR + 4 * (r16 & 3)];
+        if (VT) {
 #pragma unroll
-        for (int db = 0; db < DP / 16; ++db) {
-            const bf16x8 a = join_tr(lds_read_tr(vb + db * 16), lds_read_tr(vb + db * 16 + 4 * VSTR));
-            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
+            for (int db = 0; db < DP / 16; ++db)
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv[db]), pk, o[db], 0, 0, 0);
+        } else {
+            lds_wave_fence(); // this tile's V is in LDS before the transposed reads
+            const uint16_t *vb = &vt[(8 * grp + (r16 >> 2)) * VSTR + 4 * (r16 & 3)];
+#pragma unroll
+            for (int db = 0; db < DP / 16; ++db) {
+                const bf16x8 a =
+                    join_tr(lds_read_tr(vb + db * 16), lds_read_tr(vb + db * 16 + 4 * VSTR));
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
+            }
         }
     }
     l_run += __shfl_xor(l_run, 16);
@@ -738,19 +831,24 @@ __global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__rest
     }
 }
 
-template <int DP, int KT, bool CAUSAL, bool VEC>
+// Calls f(std::integral_constant<bool, b>{}): turns a runtime flag into a template argument.
+template <typename F> hipError_t with_flag(bool b, F &&f) {
+    return b ? f(std::true_type{}) : f(std::false_type{});
+}
+
+template <int DP, int KT, bool CAUSAL, bool VEC, bool VT>
 hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, float c, hipStream_t st) {
     const int nqt = (Sq + 127) / 128;
     const long nblk = (long)Hq * nqt;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_kernel<DP, KT, CAUSAL, VEC>), dim3((unsigned)nblk), dim3(256),
-                       0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt);
+    hipLaunchKernelGGL((attn_prefill_kernel<DP, KT, CAUSAL, VEC, VT>), dim3((unsigned)nblk),
+                       dim3(256), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt);
     return hipGetLastError();
 }
 
-template <int DP, int KT, int NW, bool CAUSAL>
+template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   float *O, int Hq, int Hkv, int Sq, int Sk, float c,
                                   hipStream_t st) {
@@ -758,7 +856,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
     const long nblk = (long)Hq * nqt;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL>), dim3((unsigned)nblk),
+    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, c, nqt);
     return hipGetLastError();
 }
@@ -774,41 +872,49 @@ static int prefill_waves() {
     return nw;
 }
 
-template <int DP, int KT, bool CAUSAL>
+template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, float c, hipStream_t st) {
     if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
         if (prefill_waves() == 8)
-            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
-    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
+                                                                 st);
+    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
 }
 
+// The fast kernel needs D == DP, 16-byte vectors (vec; with V^T also Sk % 8 == 0, which the host
+// folds into vec) and a kv head's bytes within a buffer's 31-bit range.
 template <int DP, int KT>
 hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, float c,
-                             hipStream_t st) {
-    if (vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL)
-        return causal ? launch_prefill_fast_t<DP, KT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st)
-                      : launch_prefill_fast_t<DP, KT, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
-    if (causal)
-        return vec ? launch_prefill_t<DP, KT, true, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st)
-                   : launch_prefill_t<DP, KT, true, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
-    return vec ? launch_prefill_t<DP, KT, false, true>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st)
-               : launch_prefill_t<DP, KT, false, false>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
+                             float c, hipStream_t st) {
+    const bool fast = vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL;
+    return with_flag(causal != 0, [&](auto CA) {
+        return with_flag(vt != 0, [&](auto VTF) {
+            constexpr bool kC = decltype(CA)::value, kT = decltype(VTF)::value;
+            if (fast)
+                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+            return with_flag(vec != 0, [&](auto VE) {
+                return launch_prefill_t<DP, KT, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
+                                                                              Sq, Sk, D, c, st);
+            });
+        });
+    });
 }
 
 template <int DP>
 hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                            int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int kt,
-                            float c, hipStream_t st) {
+                            int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
+                            int kt, float c, hipStream_t st) {
     switch (kt) {
     case 32:
-        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
     case 64:
-        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
     case 128:
         if constexpr (DP <= 64)
-            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, c, st);
+            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
+                                              st);
         return hipErrorInvalidValue;
     default:
         return hipErrorInvalidValue;
@@ -818,43 +924,40 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
 template <int DP>
 hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
-                           int D, int causal, int vec, float c, int nsplit, int kps,
+                           int D, int causal, int vec, int vt, float c, int nsplit, int kps,
                            hipStream_t st) {
     const long nblk = (long)Hkv * nsplit;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
-    dim3 grid((unsigned)nblk), block(256);
-    if (causal) {
-        if (vec)
-            hipLaunchKernelGGL((attn_decode_kernel<DP, true, true>), grid, block, 0, st, Q, K, V,
-                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
-        else
-            hipLaunchKernelGGL((attn_decode_kernel<DP, true, false>), grid, block, 0, st, Q, K, V,
-                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
-    } else {
-        if (vec)
-            hipLaunchKernelGGL((attn_decode_kernel<DP, false, true>), grid, block, 0, st, Q, K, V,
-                               O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
-        else
-            hipLaunchKernelGGL((attn_decode_kernel<DP, false, false>), grid, block, 0, st, Q, K,
-                               V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
-    }
-    return hipGetLastError();
+    return with_flag(causal != 0, [&](auto CA) {
+        return with_flag(vec != 0, [&](auto VE) {
+            return with_flag(vt != 0, [&](auto VTF) {
+                hipLaunchKernelGGL((attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
+                                                       decltype(VTF)::value>),
+                                   dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl,
+                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+                return hipGetLastError();
+            });
+        });
+    });
 }
 
 } // namespace
 
 // ---- extern "C" launchers called by the C host layer (attn_flash.c) -------------------------
+// vt = 1: V is V^T [Hkv][D][Sk] (pack_v_full's layout); vec must then also imply Sk % 8 == 0.
 extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                        float *O, int Hq, int Hkv, int Sq, int Sk, int D,
-                                       int causal, int vec, int dp, int kt, float c,
+                                       int causal, int vec, int vt, int dp, int kt, float c,
                                        void *stream) {
     hipStream_t st = (hipStream_t)stream;
     switch (dp) {
     case 64:
-        return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, kt, c, st);
+        return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+                                         st);
     case 128:
-        return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, kt, c, st);
+        return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+                                          st);
     default:
         return (int)hipErrorInvalidValue;
     }
@@ -862,16 +965,16 @@ extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, con
 
 extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                       float *O, float *pm, float *pl, float *pacc, int Hq,
-                                      int Hkv, int Sq, int Sk, int D, int causal, int vec, int dp,
-                                      float c, int nsplit, int kps, void *stream) {
+                                      int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
+                                      int dp, float c, int nsplit, int kps, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     switch (dp) {
     case 64:
         return (int)launch_decode_d<64>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal, vec,
-                                        c, nsplit, kps, st);
+                                        vt, c, nsplit, kps, st);
     case 128:
         return (int)launch_decode_d<128>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal,
-                                         vec, c, nsplit, kps, st);
+                                         vec, vt, c, nsplit, kps, st);
     default:
         return (int)hipErrorInvalidValue;
     }
