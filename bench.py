@@ -49,19 +49,47 @@ def make_inputs(ts, B, Hq, Hkv, Sq, Sk, D, seed, sigma_q=1.0, copies=1):
     return bufs
 
 
-def time_calls(ts, bufs, B, Hq, Hkv, Sq, Sk, D, causal, bk, scratch, steps, warmup):
-    """Returns (wall ms per step, HIP-event kernel ms per step)."""
+def prepack(ts, bufs, B, Hkv, Sk, D):
+    """Replace each copy's row-major V by V^T [Hkv][D][Sk] made on the device by pack_v_full
+    (the operator the reference runs outside the timed attention, flash.c:1070-1089)."""
+    out = []
+    for q, k, v, o, host in bufs:
+        vp = ts.DeviceBuffer(v.nbytes)
+        ts.pack_v_full(v, vp, B * Hkv, Sk, D)
+        ts.synchronize()
+        v.free()
+        out.append((q, k, vp, o, host))
+    return out
+
+
+def time_pack_v(ts, bufs, B, Hkv, Sk, D, steps=20):
+    """Kernel ms of one pack_v_full over the workload's V (HIP events)."""
+    v = bufs[0][2]
+    with ts.DeviceBuffer(v.nbytes) as vp:
+        ts.pack_v_full(v, vp, B * Hkv, Sk, D)
+        ts.synchronize()
+        e0, e1 = ts.Event(), ts.Event()
+        e0.record()
+        for _ in range(steps):
+            ts.pack_v_full(v, vp, B * Hkv, Sk, D)
+        e1.record()
+        ts.synchronize()
+        return e0.elapsed_ms(e1) / steps
+
+
+def time_calls(ts, bufs, B, Hq, Hkv, Sq, Sk, D, causal, bk, scratch, steps, warmup, vp=0):
+    """Returns (wall ms per step, HIP-event kernel ms per step). vp=1: V buffers hold V^T."""
     n = len(bufs)
     for i in range(warmup):
         q, k, v, o, _ = bufs[i % n]
-        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch)
+        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch, vp)
     ts.synchronize()
     e0, e1 = ts.Event(), ts.Event()
     t0 = time.perf_counter()
     e0.record()
     for i in range(steps):
         q, k, v, o, _ = bufs[i % n]
-        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch)
+        ts.attn_flash(q, k, v, o, B * Hq, B * Hkv, Sq, Sk, D, causal, bk, scratch, vp)
     e1.record()
     ts.synchronize()
     t1 = time.perf_counter()
@@ -181,12 +209,34 @@ def main():
     head_parity = parity(ts, o, bufs, B, Hq, Hkv, S, S, D, 0, 8, nthreads)
     log("headline: %.3f ms/step wall, %.3f ms kernel -> %.1f TFLOP/s (%.1f%% of peak); %s" %
         (wall_ms, kern_ms, achieved, 100 * achieved / MFMA_BF16_PEAK_TFLOPS, head_parity))
-    for b in bufs:
-        for x in b[:4]:
-            x.free()
     traffic = traffic_from_profiles("attn_prefill_c3_4k_traffic.txt")
 
     extra = {}
+    if not args.no_extra:
+        # ---- the same workload, causal (useful work = unmasked pairs only) ---------------------
+        cflops = 4.0 * B * Hq * D * (S * (S + 1) // 2)
+        w, k = time_calls(ts, bufs, B, Hq, Hkv, S, S, D, 1, args.bk, scratch, 20, 3)
+        pc = parity(ts, o, bufs, B, Hq, Hkv, S, S, D, 1, 8, nthreads)
+        extra["c3_gqa_prefill_4k_causal"] = {
+            "kernel_ms": k, "TFLOP_s": cflops / (k * 1e-3) / 1e12,
+            "mfma_frac": cflops / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "flop_note": "4*D per unmasked (q,k) pair", "parity": pc}
+        log("c3 4k causal:", extra["c3_gqa_prefill_4k_causal"])
+        # ---- the same workload with a pre-packed V^T (v_prepacked=1) ---------------------------
+        pk_ms = time_pack_v(ts, bufs, B, Hkv, S, D)
+        bufs = prepack(ts, bufs, B, Hkv, S, D)
+        w, k = time_calls(ts, bufs, B, Hq, Hkv, S, S, D, 0, args.bk, scratch, 20, 3, vp=1)
+        pv = parity(ts, o, bufs, B, Hq, Hkv, S, S, D, 0, 8, nthreads)
+        extra["c3_gqa_prefill_4k_v_prepacked"] = {
+            "kernel_ms": k, "TFLOP_s": flops / (k * 1e-3) / 1e12,
+            "mfma_frac": flops / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "pack_v_full_ms": pk_ms,
+            "pack_v_full_GB_s": 2 * B * Hkv * S * D * 2 / (pk_ms * 1e-3) / 1e9, "parity": pv}
+        log("c3 4k v_prepacked:", extra["c3_gqa_prefill_4k_v_prepacked"])
+    for b in bufs:
+        for x in b[:4]:
+            x.free()
+
     if not args.no_extra:
         # ---- config 2: GQA decode (HBM-bound) ------------------------------------------------
         Bd, Hqd, Hkvd, Skd, Dd = 64, 32, 8, 4096, 128
@@ -201,6 +251,13 @@ def main():
                                   "traffic": traffic_from_profiles(
                                       "attn_decode_c2_traffic.txt")}
         log("c2 decode:", extra["c2_gqa_decode"])
+        db = prepack(ts, db, Bd, Hkvd, Skd, Dd)
+        w, k = time_calls(ts, db, Bd, Hqd, Hkvd, 1, Skd, Dd, 0, args.bk, scratch, 50, 5, vp=1)
+        extra["c2_gqa_decode_v_prepacked"] = {
+            "kernel_us": k * 1e3, "GB_s": dbytes / (k * 1e-3) / 1e9,
+            "hbm_frac": dbytes / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "parity": parity(ts, o, db, Bd, Hqd, Hkvd, 1, Skd, Dd, 0, 0, nthreads)}
+        log("c2 decode v_prepacked:", extra["c2_gqa_decode_v_prepacked"])
         for b in db:
             for x in b[:4]:
                 x.free()
