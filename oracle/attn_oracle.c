@@ -27,6 +27,8 @@
  *
  * Build: oracle/Makefile (gcc -O2, no -ffast-math: the summation order is the point).
  */
+#include "attn_oracle.h"
+
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
