@@ -27,8 +27,11 @@ TOOL_SOURCES = {"roofline_bench": "roofline_bench.hip"}
 C_SOURCES = ["attn_flash.c", "attn_devutil.c", "attn_synth.c"]
 
 # Packed fp32 VALU forms are disabled for all device code on this platform.
+# IEEE mode off (with NaNs not honoured): fmaxf lowers to a bare v_max/v_max3 instead of
+# canonicalising each MFMA result first. A NaN input still reaches O through the products.
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-mno-amdgpu-ieee", "-fno-honor-nans",
                "-I" + INCLUDE]
 CC_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-fopenmp",
             "-I" + INCLUDE, "-I" + os.path.join(ROCM, "include")]

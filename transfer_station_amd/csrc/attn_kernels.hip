@@ -359,8 +359,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 // ------------------------------------------------------------------------------------------
 constexpr float kLazyLog2 = 8.0f;
 
+// The descriptor must live in scalar registers; its inputs are workgroup-uniform, and the
+// readfirstlane makes that explicit so the compiler never falls back to a per-lane loop.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    void *p = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes),
                                              0x00020000);
 }
 
@@ -518,17 +524,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
             // Row max of the tile as a shallow tree (independent max3 leaves, then a combine),
             // the partner half-row through the VALU exchange, then the wave-uniform lazy-rescale
             // test; the exponentials and the P.V MFMAs follow in one branch-free block.
-            float mt[KT / 32][4];
+            // Independent chains of 8 scores (max3, max3, max3, max: two new values per
+            // instruction), combined at the end.
+            float mt[KT / 16];
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    mt[t][q] = fmaxf(fmaxf(s[t][4 * q], s[t][4 * q + 1]),
-                                     fmaxf(s[t][4 * q + 2], s[t][4 * q + 3]));
-            float mx = kNegInf;
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int b = 8 * hh;
+                    float m = fmaxf(s[t][b], fmaxf(s[t][b + 1], s[t][b + 2]));
+                    m = fmaxf(m, fmaxf(s[t][b + 3], s[t][b + 4]));
+                    m = fmaxf(m, fmaxf(s[t][b + 5], s[t][b + 6]));
+                    mt[2 * t + hh] = fmaxf(m, s[t][b + 7]);
+                }
+            float mx = mt[0];
 #pragma unroll
-            for (int t = 0; t < KT / 32; ++t)
-                mx = fmaxf(mx, fmaxf(fmaxf(mt[t][0], mt[t][1]), fmaxf(mt[t][2], mt[t][3])));
+            for (int j = 1; j < KT / 16; j += 2)
+                mx = (j + 1 < KT / 16) ? fmaxf(mx, fmaxf(mt[j], mt[j + 1])) : fmaxf(mx, mt[j]);
             mx = max_xor32(mx);
             const bool raise = mx > m_run + lazy_raw;
             if (__builtin_amdgcn_ballot_w64(raise) != 0) {
