@@ -181,6 +181,8 @@ def main():
     ap.add_argument("--bk", type=int, default=128)
     ap.add_argument("--no-extra", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-peaks", action="store_true",
+                    help="skip the roofline microbenchmark (e.g. under a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         sys.exit("bench.py: this build measures ONE GPU only (the path shards over (batch, "
@@ -284,7 +286,7 @@ def main():
                     x.free()
             sc.free()
 
-    peaks = measured_peaks()
+    peaks = {} if args.no_peaks else measured_peaks()
     log("measured peaks:", peaks)
     cpu = None if args.no_cpu else cpu_baseline(o, ts)
     if cpu:

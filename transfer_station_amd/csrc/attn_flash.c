@@ -123,14 +123,14 @@ void *attn_flash_get_stream(void) { return t_stream; }
 
 /* ---- tile and split selection ------------------------------------------------------------ */
 /* Key-tile size of the prefill kernel for the caller's bk: the online-softmax update runs
- * once per KT keys. bk below 32 (one 32-key MFMA tile) runs at KT=32; a bk above the largest
- * tile that still fits two waves per SIMD (64 keys at D<=128 > 64, 128 keys at D<=64) is
- * processed as sub-blocks of that size, each its own update (the result is bk-invariant
- * within the tolerance, as in the reference). */
+ * once per KT keys. bk below 32 (one 32-key MFMA tile) runs at KT=32, bk=64 at 64, and a bk
+ * of 128 or more at 128 keys, the largest tile that still fits two waves per SIMD; a larger
+ * bk is processed as 128-key sub-blocks, each its own update (the result is bk-invariant
+ * within the tolerance, as in the reference). The general (odd-D or unaligned) kernel caps
+ * its tile at 64 keys for D > 64. */
 static int attn_kt_for_bk(int bk, int dp) {
-    const int kt_max = (dp == 128) ? 64 : 128; /* largest tile that keeps 2 waves per SIMD */
-    int kt = (bk <= 32) ? 32 : (bk == 64 ? 64 : 128);
-    return kt < kt_max ? kt : kt_max;
+    (void)dp;
+    return (bk <= 32) ? 32 : (bk == 64 ? 64 : 128);
 }
 
 #define ATTN_DECODE_ROWS 16 /* query rows per kv head the decode MFMA tile holds */

@@ -896,10 +896,13 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
 
 // The fast kernel needs D == DP, 16-byte vectors (vec; with V^T also Sk % 8 == 0, which the host
 // folds into vec) and a kv head's bytes within a buffer's 31-bit range.
+// The general kernel keeps a 64-key tile at DP = 128: its 4-wave tiling at 128 keys would need
+// all 256 registers and drop to one wave per SIMD.
 template <int DP, int KT>
 hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                              int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
                              float c, hipStream_t st) {
+    constexpr int KTG = (DP == 128 && KT == 128) ? 64 : KT;
     const bool fast = vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL;
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vt != 0, [&](auto VTF) {
@@ -907,8 +910,8 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
             if (fast)
                 return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
             return with_flag(vec != 0, [&](auto VE) {
-                return launch_prefill_t<DP, KT, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
-                                                                              Sq, Sk, D, c, st);
+                return launch_prefill_t<DP, KTG, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
+                                                                               Sq, Sk, D, c, st);
             });
         });
     });
@@ -924,10 +927,7 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
     case 64:
         return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
     case 128:
-        if constexpr (DP <= 64)
-            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
-                                              st);
-        return hipErrorInvalidValue;
+        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
     default:
         return hipErrorInvalidValue;
     }
