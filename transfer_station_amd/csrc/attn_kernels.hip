@@ -493,23 +493,31 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
         const int kbase = kt * KT;
         if (kbase <= wave_maxkey) {
             f32x16 s[KT / 32];
+            const uint16_t *kb0 = &Ks[buf][kperm * KSTR + hi * 8];
+            bf16x8 ka[2][DP / 16];
+#pragma unroll
+            for (int kk = 0; kk < DP / 16; ++kk)
+                ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * 16));
+            __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
                     s[t][i] = 0.f;
-                // All K fragments of this 32-key sub-tile are read as one group ahead of its
-                // MFMA chain, so the LDS latency is paid once per sub-tile.
-                const uint16_t *kb = &Ks[buf][(t * 32 + kperm) * KSTR + hi * 8];
-                bf16x8 ka[DP / 16];
+                // The next sub-tile's K fragments are read between this sub-tile's MFMAs.
 #pragma unroll
-                for (int kk = 0; kk < DP / 16; ++kk)
-                    ka[kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb + kk * 16));
+                for (int kk = 0; kk < DP / 16; ++kk) {
+                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
+                    if (t + 1 < KT / 32)
+                        ka[(t + 1) & 1][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                            kb0 + (t + 1) * 32 * KSTR + kk * 16));
+                }
 #pragma unroll
-                for (int kk = 0; kk < DP / 16; ++kk)
-                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk], qb[kk], s[t], 0, 0, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0); // DS reads
-                __builtin_amdgcn_sched_group_barrier(0x008, DP / 16, 0); // MFMAs
+                for (int kk = 0; kk < DP / 16; ++kk) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (t + 1 < KT / 32)
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
             }
             if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + q0)) {
 #pragma unroll
