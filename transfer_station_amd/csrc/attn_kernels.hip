@@ -626,7 +626,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 // ------------------------------------------------------------------------------------------
 // Decode (split-K). One workgroup per (kv head u, split sp) serves all M = g*Sq <= 16 query
 // rows of that kv head from ONE read of its K/V range [sp*kps, min(sp*kps+kps, Sk)). Waves
-// take interleaved 32-key tiles; per tile (v_mfma_f32_16x16x32_bf16):
+// take interleaved 32-key tiles, starting at a workgroup-dependent 128-key step; per tile
+// (v_mfma_f32_16x16x32_bf16):
 //   S^T[key][row] = K . Q^T  (A = K rows loaded from global straight into the operand layout)
 //   O^T[d][row]  += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from a wave-private LDS tile)
 // The 4 waves merge in LDS; the workgroup writes O directly (nsplit == 1) or one partial
@@ -674,7 +675,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     uint16_t *vt = &Vw[w * VTILE];
-    for (int tb = k0 + w * 32; tb < k1; tb += 128) {
+    // Each workgroup starts its walk over the 128-key steps at a different step: workgroups
+    // then read different column ranges at the same time, which spreads a V^T input's
+    // 2*Sk-byte-strided rows over more HBM channels.
+    const int nsteps = (k1 - k0 + 127) / 128;
+    const int rot = (int)blockIdx.x % (nsteps > 0 ? nsteps : 1);
+    for (int js = 0; js < nsteps; ++js) {
+        const int step = (js + rot < nsteps) ? js + rot : js + rot - nsteps;
+        const int tb = k0 + step * 128 + w * 32;
+        if (tb >= k1)
+            continue;
         u32x4 ka[2][DP / 32];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
