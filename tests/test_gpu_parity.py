@@ -136,13 +136,16 @@ def test_qwen3_causal_long(oracle):
 
 
 # ---- tails, head_dim, masks -----------------------------------------------------------------------
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [0, 1])
 @pytest.mark.parametrize("bk", [32, 64, 128])
-def test_tail_probe(oracle, bk, causal):
+def test_tail_probe(oracle, bk, causal, D):
+    """The reference's tail probe (README:550-554): Sk around multiples of bk, both head sizes
+    the fast kernel is built for."""
     for Sk in (1, bk - 1, bk, bk + 1, 2 * bk, 2 * bk + 1, 70):
         for Sq in (40, 1):
-            Q, K, V = ts.synth_lcg_qkv(4, 2, Sq, Sk, 64)
-            check(oracle, "tail", Q, K, V, 4, 2, Sq, Sk, 64, causal, bk)
+            Q, K, V = ts.synth_lcg_qkv(4, 2, Sq, Sk, D)
+            check(oracle, "tail", Q, K, V, 4, 2, Sq, Sk, D, causal, bk)
 
 
 @pytest.mark.parametrize("D", [1, 2, 3, 7, 8, 16, 24, 33, 40, 63, 64, 65, 72, 100, 127, 128])
@@ -243,6 +246,7 @@ VT_CASES = [
     # name, Hq, Hkv, Sq, Sk, D, causal, bk
     ("fast D128 partial tile", 8, 2, 300, 1000, 128, 0, 128),
     ("fast D128 causal", 8, 2, 513, 1024, 128, 1, 64),
+    ("fast D128 kt128 causal", 8, 2, 700, 1000, 128, 1, 128),
     ("fast D64 kt128 causal", 4, 4, 257, 520, 64, 1, 256),
     ("fast D64 kt32 Sk<KT", 4, 2, 100, 24, 64, 0, 16),
     ("general D40 causal", 6, 3, 130, 70, 40, 1, 128),
@@ -283,6 +287,27 @@ def test_v_prepacked_c3_4k(oracle):
     assert np.array_equal(packed.view(np.uint32), base.view(np.uint32))
     check(oracle, "v_prepacked c3 4k", Q, K, V, B * Hq, B * Hkv, S, S, D, 0, 128, ref_cap=8,
           O=packed)
+
+
+def test_scratch_canary():
+    """Nothing is written past attn_flash_scratch_bytes (the reference's canary guard,
+    EXEC_LOG:517-569): 64 KiB of 0x5A after the block must survive split decode, merge and
+    prefill calls at every bk."""
+    D = 128
+    sbytes = ts.attn_flash_scratch_bytes(D, 4096)
+    guard = 64 << 10
+    cases = [(32, 1, 1, 4096, 0), (8, 2, 4, 3000, 1), (8, 2, 300, 1000, 1)]
+    with ts.DeviceBuffer(sbytes + guard) as ds:
+        ds.fill_bytes(0x5A)
+        for bk in (16, 128, 4096):
+            for Hq, Hkv, Sq, Sk, causal in cases:
+                Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 31)
+                with ts.DeviceBuffer.from_array(Q) as dq, ts.DeviceBuffer.from_array(K) as dk, \
+                        ts.DeviceBuffer.from_array(V) as dv, ts.DeviceBuffer(Hq * Sq * D * 4) as do:
+                    ts.attn_flash(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, causal, bk, ds)
+                    ts.synchronize()
+        tail = ds.download(np.uint8)[sbytes:]
+    assert tail.size == guard and np.all(tail == 0x5A)
 
 
 def test_timing_struct_and_scratch_reuse(oracle):
