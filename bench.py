@@ -164,13 +164,25 @@ def cpu_baseline(o, ts, budget_s=12.0):
         out[label] = {"rows": nrows, "seconds": dt, "tflops": nrows * flop_per_row / dt / 1e12,
                       "threads": nt}
     allc = out["all"]
+    full_flop = 4.0 * B * Hq * S * S * D
+    # config 2 (decode) is small enough to run whole on the CPU: every row, all threads
+    Bd, Hqd, Hkvd, Skd, Dd = 64, 32, 8, 4096, 128
+    Qd, Kd, Vd = ts.synth_normal_qkv(Bd * Hqd, Bd * Hkvd, 1, Skd, Dd, SEED0 + 2)
+    t0 = time.perf_counter()
+    o.attn_ref(Qd, Kd, Vd, Bd * Hqd, Bd * Hkvd, 1, Skd, Dd, 0, nthreads=nthreads)
+    c2_s = time.perf_counter() - t0
     return {"value": allc["tflops"], "unit": "TFLOP/s", "cores": allc["threads"],
             "kind": "port",
             "sample": "oracle attn_ref (flash.c:262-314 restated in C, gcc -O2, OpenMP over "
                       "(head,row)) on %d spread query rows of config 3 @4k (Sk=4096, D=128), "
                       "%.2f s; single-thread: %.4f TFLOP/s on %d rows" %
                       (allc["rows"], allc["seconds"], out["1"]["tflops"], out["1"]["rows"]),
-            "value_1core": out["1"]["tflops"]}
+            "value_1core": out["1"]["tflops"],
+            "c3_4k_full_problem_seconds_extrapolated": {
+                "all_threads": full_flop / (allc["tflops"] * 1e12),
+                "single_thread": full_flop / (out["1"]["tflops"] * 1e12)},
+            "c2_decode_full_problem_seconds_measured": {"all_threads": c2_s,
+                                                        "threads": nthreads}}
 
 
 def main():

@@ -199,3 +199,49 @@ def test_oracle_rejects_bad_shapes(oracle):
     Q = np.zeros(64, np.uint16)
     with pytest.raises(ValueError):
         oracle.attn_ref(Q, Q, Q, 3, 2, 1, 1, 8, 0)
+
+
+# ---- a second, independent library restatement: torch SDPA in float64 on the CPU -------------
+TORCH_CASES = [
+    # Hq, Hkv, Sq, Sk, D, causal
+    (4, 4, 8, 8, 64, 0),
+    (8, 2, 37, 53, 40, 1),   # Sk > Sq: bottom-right causal keeps Sk-Sq extra keys per row
+    (6, 3, 130, 70, 40, 1),  # Sk < Sq: the first 60 rows attend nothing
+    (8, 1, 5, 200, 128, 0),  # MQA
+    (4, 2, 1, 300, 128, 1),  # decode row
+]
+
+
+@pytest.mark.parametrize("case", TORCH_CASES, ids=[str(c) for c in TORCH_CASES])
+def test_oracle_vs_torch_sdpa_float64(oracle, case):
+    """The oracle against torch.nn.functional.scaled_dot_product_attention (float64, GQA by
+    explicit head repetition, bottom-right causal mask built explicitly, fully masked rows
+    set to 0 as flash.c:851-860 writes them). Independent of the numpy fixtures."""
+    torch = pytest.importorskip("torch")
+    Hq, Hkv, Sq, Sk, D, causal = case
+    Q, K, V = oracle.normal_qkv(Hq, Hkv, Sq, Sk, D, seed=4242 + Sq)
+    R = oracle.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, causal).reshape(Hq, Sq, D).astype(np.float64)
+    f = lambda x, H, S: torch.from_numpy(oracle.bf16_to_f32(x).astype(np.float64).reshape(H, S, D))
+    q, k, v = f(Q, Hq, Sq), f(K, Hkv, Sk), f(V, Hkv, Sk)
+    g = Hq // Hkv
+    k = k.repeat_interleave(g, dim=0)
+    v = v.repeat_interleave(g, dim=0)
+    i = torch.arange(Sq).unsqueeze(1)
+    j = torch.arange(Sk).unsqueeze(0)
+    allowed = (j <= Sk - Sq + i) if causal else torch.ones(Sq, Sk, dtype=torch.bool)
+    bias = torch.zeros(Sq, Sk, dtype=torch.float64).masked_fill(~allowed, float("-inf"))
+    s = (q @ k.transpose(1, 2)) * (1.0 / np.sqrt(np.float32(D)).astype(np.float64)) + bias
+    empty = ~allowed.any(dim=1)
+    s[:, empty, :] = 0.0  # keep softmax finite on rows that attend nothing; zeroed below
+    T = torch.softmax(s, dim=-1) @ v
+    T[:, empty, :] = 0.0
+    T = T.numpy()
+    scale = np.abs(T).max()
+    err = np.abs(R - T).max() / scale
+    assert np.isfinite(R).all() and err < 1e-5, err
+    # The same comparison through SDPA itself where no row is empty.
+    if not bool(empty.any()):
+        sd = torch.nn.functional.scaled_dot_product_attention(
+            q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), attn_mask=allowed,
+            scale=float(1.0 / np.sqrt(np.float32(D)))).squeeze(0).numpy()
+        assert np.abs(R - sd).max() / np.abs(sd).max() < 1e-5
