@@ -892,21 +892,25 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 }
 
 // Waves per workgroup for the fast prefill kernel: 8 (256 query rows, one workgroup per CU,
-// two waves per SIMD) unless ATTN_PREFILL_WAVES=4 selects 4 for tuning sweeps.
-static int prefill_waves() {
-    static int nw = -1;
-    if (nw < 0) {
+// two waves per SIMD), or 4 (128 rows) when 256-row tiles would leave most CUs without a
+// workgroup (fewer than 64 of them: measured 9.1 -> 6.8 us on 4 heads x 256 rows).
+// ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
+static int prefill_waves(int Hq, int Sq) {
+    static int forced = -1;
+    if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
-        nw = (e && atoi(e) == 4) ? 4 : 8;
+        forced = (e && (atoi(e) == 4 || atoi(e) == 8)) ? atoi(e) : 0;
     }
-    return nw;
+    if (forced)
+        return forced;
+    return ((long)Hq * ((Sq + 255) / 256) < 64) ? 4 : 8;
 }
 
 template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, float c, hipStream_t st) {
     if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
-        if (prefill_waves() == 8)
+        if (prefill_waves(Hq, Sq) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
                                                                  st);
     return launch_prefill_fast_nw<DP, KT, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
