@@ -226,14 +226,27 @@ def test_bk_invariance(oracle):
 
 
 # ---- the other entry points ------------------------------------------------------------------------
-def test_pack_v_full_transposes_exactly():
-    Hkv, Sk, D = 3, 77, 40
-    V = np.arange(Hkv * Sk * D, dtype=np.uint16)
-    with ts.DeviceBuffer.from_array(V) as dv, ts.DeviceBuffer(V.nbytes) as dp:
-        ts.pack_v_full(dv, dp, Hkv, Sk, D)
+@pytest.mark.parametrize("Hkv,Sk,D,offset", [
+    (3, 77, 40, 0),     # element-wise path (Sk % 8 != 0)
+    (3, 80, 40, 0),     # 16-byte path, partial 64-column tile
+    (1, 200, 64, 0),    # 16-byte path, partial 64-key tile
+    (2, 4096, 128, 0),  # 16-byte path, full tiles
+    (2, 8, 8, 0),       # 16-byte path, one chunk per row
+    (2, 64, 64, 2),     # misaligned by one element: element-wise path
+])
+def test_pack_v_full_transposes_exactly(Hkv, Sk, D, offset):
+    rng = np.random.default_rng(Sk * 1000 + D)
+    V = rng.integers(0, 1 << 16, size=Hkv * Sk * D, dtype=np.uint16)
+    guard = 256
+    with ts.DeviceBuffer(V.nbytes + offset) as dv, ts.DeviceBuffer(V.nbytes + offset + guard) as dp:
+        dv.upload(np.concatenate([np.zeros(offset // 2, np.uint16), V]))
+        dp.fill_bytes(0x5A)
+        ts.pack_v_full(dv.ptr + offset, dp.ptr + offset, Hkv, Sk, D)
         ts.synchronize()
-        got = dp.download(np.uint16).reshape(Hkv, D, Sk)
+        raw = dp.download(np.uint8)
+        got = raw[offset:offset + V.nbytes].view(np.uint16).reshape(Hkv, D, Sk)
     assert np.array_equal(got, V.reshape(Hkv, Sk, D).transpose(0, 2, 1))
+    assert np.all(raw[:offset] == 0x5A) and np.all(raw[offset + V.nbytes:] == 0x5A)
 
 
 # ---- v_prepacked = 1: V^T [Hkv][D][Sk] input (flash.c:751-753,770,812-833) -----------------------

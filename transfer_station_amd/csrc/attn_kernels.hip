@@ -17,7 +17,8 @@
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 128 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 16 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
-//   attn_pack_v_kernel                     V [Hkv][Sk][D] -> V^T [Hkv][D][Sk]
+//   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
+//                                          vector path / any shape)
 // VT selects a pre-transposed V ([Hkv][D][Sk], pack_v_full's layout).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -861,6 +862,47 @@ __global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__rest
     }
 }
 
+// V [Hkv][Sk][D] -> Vp [Hkv][D][Sk] when D % 8 == 0, Sk % 8 == 0 and both tensors are 16-byte
+// aligned: one workgroup per 64-key x 64-column tile. Key rows arrive as 16-byte loads into LDS;
+// each thread then gathers 8 consecutive keys of one column and stores them as one 16-byte
+// chunk, so each wave store writes 8 columns x 128 contiguous bytes.
+__global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__restrict__ V,
+                                                            uint16_t *__restrict__ Vp, int Sk,
+                                                            int D) {
+    constexpr int TK = 64, TD = 64, PITCH = TD + 8; // 144-byte rows: 16-byte aligned writes
+    __shared__ __attribute__((aligned(16))) uint16_t tile[TK * PITCH];
+    const int kv = blockIdx.z;
+    const int k0 = blockIdx.x * TK, d0 = blockIdx.y * TD;
+    const uint16_t *src = V + (size_t)kv * Sk * D;
+    uint16_t *dst = Vp + (size_t)kv * D * Sk;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int cidx = tid + 256 * r;
+        const int row = cidx >> 3, ch = cidx & 7;
+        const int k = k0 + row, d = d0 + ch * 8;
+        u32x4 v = zero4();
+        if (k < Sk && d < D)
+            v = *reinterpret_cast<const u32x4 *>(src + (size_t)k * D + d);
+        *reinterpret_cast<u32x4 *>(&tile[row * PITCH + ch * 8]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int dl = r * 32 + (tid >> 3), kc = (tid & 7) * 8;
+        const int d = d0 + dl, k = k0 + kc;
+        if (d < D && k < Sk) {
+            uint32_t e[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                e[j] = tile[(kc + j) * PITCH + dl];
+            const u32x4 out = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                               e[6] | (e[7] << 16)};
+            *reinterpret_cast<u32x4 *>(dst + (size_t)d * Sk + k) = out;
+        }
+    }
+}
+
 // Calls f(std::integral_constant<bool, b>{}): turns a runtime flag into a template argument.
 template <typename F> hipError_t with_flag(bool b, F &&f) {
     return b ? f(std::true_type{}) : f(std::false_type{});
@@ -1028,6 +1070,12 @@ extern "C" int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, 
                                       void *stream) {
     if (Hkv <= 0 || Sk <= 0 || D <= 0 || Hkv > 65535)
         return (int)hipErrorInvalidValue;
+    if (D % 8 == 0 && Sk % 8 == 0 && (((uintptr_t)V | (uintptr_t)Vp) & 15u) == 0) {
+        dim3 grid((unsigned)((Sk + 63) / 64), (unsigned)((D + 63) / 64), (unsigned)Hkv);
+        hipLaunchKernelGGL(attn_pack_v16_kernel, grid, dim3(256), 0, (hipStream_t)stream, V, Vp,
+                           Sk, D);
+        return (int)hipGetLastError();
+    }
     dim3 grid((unsigned)((Sk + 31) / 32), (unsigned)((D + 31) / 32), (unsigned)Hkv);
     hipLaunchKernelGGL(attn_pack_v_kernel, grid, dim3(32, 8), 0, (hipStream_t)stream, V, Vp, Sk,
                        D);
