@@ -135,6 +135,25 @@ def test_qwen3_causal_long(oracle):
     check(oracle, "qwen3 1k causal", Q, K, V, 16, 8, 1024, 1024, 128, 1, 128, ref_cap=8)
 
 
+# ---- causal grids of at most one workgroup per CU: the heavier query tiles' key ranges are split
+# in two workgroups and merged through the scratch (Qwen3 4k uses exactly all 65536 slots) ------
+@pytest.mark.parametrize("shape", [
+    (16, 8, 4096, 4096, 128, 8),   # the reference's --long qwen3 4k
+    (16, 8, 2048, 2048, 128, 8),
+    (8, 2, 1000, 3000, 128, 0),    # Sk > Sq, every row
+    (4, 4, 700, 300, 64, 0),       # Sq > Sk: rows below Sq - Sk attend nothing
+    (6, 3, 600, 600, 40, 0),       # general kernel (D = 40): no split, same answer
+], ids=["qwen3-4k", "qwen3-2k", "sk>sq", "sq>sk", "d40"])
+def test_causal_split_small_grid(oracle, shape):
+    Hq, Hkv, Sq, Sk, D, cap = shape
+    Q, K, V = ts.synth_lcg_qkv(Hq, Hkv, Sq, Sk, D)
+    O = check(oracle, "causal small grid", Q, K, V, Hq, Hkv, Sq, Sk, D, 1, 128, ref_cap=cap)
+    if Sq > Sk:
+        assert np.all(O.reshape(Hq, Sq, D)[:, :Sq - Sk] == 0.0)
+    again = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 1, 128)
+    assert np.array_equal(O.view(np.uint32), again.view(np.uint32))
+
+
 # ---- tails, head_dim, masks -----------------------------------------------------------------------
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [0, 1])

@@ -18,21 +18,23 @@
 /* HIP launchers (attn_kernels.hip). Each returns a hipError_t. */
 int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                            int dp, int kt, float c, void *stream);
+                            int dp, int kt, float c, float *pm, float *pl, float *pacc, long slots,
+                            void *stream);
 int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
                            int D, int causal, int vec, int vt, int dp, float c, int nsplit,
                            int kps, void *stream);
 int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, float *O, int rows,
-                          int D, int nsplit, float c, void *stream);
+                          int D, int nsplit, float c, int Sq, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
 
 /* ---- device scratch layout ---------------------------------------------------------------
  * Split-K partial slots, one per (query row, split): m[ATTN_SLOTS], l[ATTN_SLOTS] and
  * acc[ATTN_SLOTS][D], each sub-buffer starting on a 256-byte boundary. The slot count is a
  * fixed capacity, so the size depends only on D (and trivially on bk), never on Sq/Sk; the
- * decode path caps its split count at ATTN_SLOTS / (Hq*Sq) and runs unsplit below 2. */
-#define ATTN_SLOTS 32768
+ * decode path caps its split count at ATTN_SLOTS / (Hq*Sq) and runs unsplit below 2, and the
+ * causal prefill splits the key range of its heavier query tiles only when their rows fit. */
+#define ATTN_SLOTS 65536
 #define ATTN_SUB_ALIGN 256
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) & ~(a - 1); }
@@ -208,11 +210,14 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
                                               causal ? 1 : 0, vec, vt, dp, c, nsplit, kps, st),
                        who);
         if (nsplit > 1)
-            attn_hip_check(attn_hip_launch_merge(cv.m, cv.l, cv.acc, O, Hq * Sq, D, nsplit, c, st),
-                           who);
+            attn_hip_check(
+                attn_hip_launch_merge(cv.m, cv.l, cv.acc, O, Hq * Sq, D, nsplit, c, Sq, st), who);
     } else {
+        struct attn_carve cv;
+        attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_prefill(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal ? 1 : 0,
-                                               vec, vt, dp, attn_kt_for_bk(bk, dp), c, st),
+                                               vec, vt, dp, attn_kt_for_bk(bk, dp), c, cv.m, cv.l,
+                                               cv.acc, ATTN_SLOTS, st),
                        who);
     }
     if (tm) {

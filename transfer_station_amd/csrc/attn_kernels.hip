@@ -379,7 +379,8 @@ template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk,
-    float c, int nqt) {
+    float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
+    float *__restrict__ pacc, int prows) {
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int D = DP;
     constexpr int NT = NW * 64; // threads per workgroup
@@ -397,12 +398,39 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 
     const int g = Hq / Hkv;
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int u = L / (g * nqt);
-    const int rr = L - u * (g * nqt);
-    // Causal work grows with the query tile, so within a kv head the last (heaviest) tiles are
-    // dispatched first: longest-first keeps the tail of the grid short.
-    const int qt = CAUSAL ? nqt - 1 - rr / g : rr / g;
-    const int h = u * g + (rr - (rr / g) * g);
+    // Work item of this workgroup: query head h, query tile qt and, for a tile whose key range
+    // is split in two (causal grids too small to fill the GPU), the half `part` (-1: whole).
+    // Causal work grows with the query tile, so the items of a kv head are dispatched heaviest
+    // first: longest-first keeps the tail of the grid short.
+    int h, qt, part = -1;
+    if (split_first < 0) {
+        const int uu = L / (g * nqt);
+        const int rr = L - uu * (g * nqt);
+        qt = CAUSAL ? nqt - 1 - rr / g : rr / g;
+        h = uu * g + (rr - (rr / g) * g);
+    } else {
+        // Per kv head: tiles qt >= split_first as two halves (work ~ (qt+1)/2 each), tiles below
+        // whole (work qt+1); item k of the merged heaviest-first order, g query heads each.
+        const int nsp = nqt - split_first;
+        const int per = g * (split_first + 2 * nsp);
+        const int uu = L / per;
+        const int rr = L - uu * per;
+        const int k = rr / g;
+        h = uu * g + (rr - k * g);
+        int ia = 0, ib = 0;
+        for (int st = 0; st < k; ++st) {
+            const bool a = ib >= split_first || (ia < 2 * nsp && nqt - ia / 2 >= 2 * (split_first - ib));
+            ia += a ? 1 : 0;
+            ib += a ? 0 : 1;
+        }
+        if (ib >= split_first || (ia < 2 * nsp && nqt - ia / 2 >= 2 * (split_first - ib))) {
+            qt = nqt - 1 - ia / 2;
+            part = ia & 1;
+        } else {
+            qt = split_first - 1 - ib;
+        }
+    }
+    const int u = h / g; // kv head
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hi = lane >> 5;
@@ -482,14 +510,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
     const int g16 = lane >> 4, i16 = lane & 15;
 
-    if (nkt > 0) {
-        gload(0);
+    // Key tiles [kt0, kt1) of this item: all of them, or one half of a split tile's range.
+    const int kt0 = (part == 1) ? nkt / 2 : 0;
+    const int kt1 = (part == 0) ? nkt / 2 : nkt;
+    if (kt0 < kt1) {
+        gload(kt0);
         swrite(0);
     }
     __syncthreads();
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nkt)
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const int buf = (kt - kt0) & 1;
+        if (kt + 1 < kt1)
             gload(kt + 1);
         const int kbase = kt * KT;
         if (kbase <= wave_maxkey) {
@@ -603,12 +634,33 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                 }
             }
         }
-        if (kt + 1 < nkt)
+        if (kt + 1 < kt1)
             swrite(buf ^ 1);
         __syncthreads();
     }
 
     const float lt = l_run + __shfl_xor(l_run, 32);
+    if (part >= 0) {
+        // Unnormalised partial of one key half: (m, l, acc) into slot (row, part) for the
+        // log-sum-exp merge (attn_merge_kernel).
+        if (myq < Sq) {
+            const size_t slot = ((size_t)h * prows + (myq - split_first * BQ)) * 2 + part;
+            if (hi == 0) {
+                pm[slot] = m_run;
+                pl[slot] = lt;
+            }
+            float *prow = pacc + slot * D;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const int d = db * 32 + i4 * 8 + 4 * hi;
+                    f32x4 v = {o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
+                    *reinterpret_cast<f32x4 *>(prow + d) = v;
+                }
+        }
+        return;
+    }
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
     if (myq < Sq) {
         float *orow = O + ((size_t)h * Sq + myq) * D;
@@ -816,13 +868,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
 }
 
-// Merge of split-K partials: one workgroup per output row (h*Sq + i).
+// Merge of split-K partials. Partial row r owns slots r*nsplit .. r*nsplit+nsplit-1 and covers
+// row q_off + r % rph of query head r / rph, so its O row is (r / rph) * Sq + q_off + r % rph
+// (decode: rph = Sq, q_off = 0). Weights w_s = 2^((m_s - max m) c), O = sum w_s acc_s / sum w_s l_s.
+__device__ __forceinline__ size_t merge_orow(long r, int rph, int q_off, int Sq) {
+    return (size_t)(r / rph) * Sq + q_off + r % rph;
+}
+
+// Any nsplit: one workgroup per partial row, threads across the columns (decode's many splits).
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ pm,
                                                          const float *__restrict__ pl,
                                                          const float *__restrict__ pacc,
                                                          float *__restrict__ O, int D, int nsplit,
-                                                         float c) {
-    const size_t row = blockIdx.x;
+                                                         float c, int rph, int q_off, int Sq) {
+    const long row = blockIdx.x;
+    const size_t orow = merge_orow(row, rph, q_off, Sq);
     const float *m = pm + row * nsplit;
     const float *l = pl + row * nsplit;
     float mx = kNegInf;
@@ -836,8 +896,45 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float acc = 0.f;
         for (int s = 0; s < nsplit; ++s)
-            acc += fast_exp2((m[s] - muse) * c) * pacc[(row * nsplit + s) * D + d];
-        O[row * D + d] = acc * inv;
+            acc += fast_exp2((m[s] - muse) * c) * pacc[((size_t)row * nsplit + s) * D + d];
+        O[orow * D + d] = acc * inv;
+    }
+}
+
+// nsplit == 2 (the causal prefill split): one wave per partial row, 4 rows per workgroup,
+// the two weights computed once per lane, columns as float2 when D is even and O 8-byte aligned.
+__global__ __launch_bounds__(256) void attn_merge2_kernel(const float *__restrict__ pm,
+                                                          const float *__restrict__ pl,
+                                                          const float *__restrict__ pacc,
+                                                          float *__restrict__ O, long rows, int D,
+                                                          float c, int rph, int q_off, int Sq) {
+    typedef __attribute__((ext_vector_type(2))) float f32x2;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows)
+        return;
+    const size_t orow = merge_orow(row, rph, q_off, Sq);
+    const float m0 = pm[2 * row], m1 = pm[2 * row + 1];
+    const float mx = fmaxf(m0, m1);
+    const float muse = (mx == kNegInf) ? 0.f : mx;
+    const float w0 = fast_exp2((m0 - muse) * c), w1 = fast_exp2((m1 - muse) * c);
+    const float lsum = w0 * pl[2 * row] + w1 * pl[2 * row + 1];
+    const float inv = (lsum > 0.f) ? 1.0f / lsum : 0.f;
+    const float a0 = w0 * inv, a1 = w1 * inv;
+    const float *p0 = pacc + (size_t)row * 2 * D, *p1 = p0 + D;
+    float *o = O + orow * D;
+    if ((D & 1) == 0 && ((uintptr_t)O & 7u) == 0) {
+        for (int d = 2 * lane; d < D; d += 128) {
+            const f32x2 x = *reinterpret_cast<const f32x2 *>(p0 + d);
+            const f32x2 y = *reinterpret_cast<const f32x2 *>(p1 + d);
+            f32x2 r;
+            r[0] = a0 * x[0] + a1 * y[0];
+            r[1] = a0 * x[1] + a1 * y[1];
+            *reinterpret_cast<f32x2 *>(o + d) = r;
+        }
+    } else {
+        for (int d = lane; d < D; d += 64)
+            o[d] = a0 * p0[d] + a1 * p1[d];
     }
 }
 
@@ -920,17 +1017,65 @@ hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t
     return hipGetLastError();
 }
 
+hipError_t launch_merge(const float *pm, const float *pl, const float *pacc, float *O, long rows,
+                        int D, int nsplit, float c, int rph, int q_off, int Sq, hipStream_t st) {
+    if (rows <= 0 || rows > 0x7fffffffL || rph <= 0)
+        return hipErrorInvalidValue;
+    if (nsplit == 2)
+        hipLaunchKernelGGL(attn_merge2_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                           pm, pl, pacc, O, rows, D, c, rph, q_off, Sq);
+    else
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(128), 0, st, pm, pl, pacc,
+                           O, D, nsplit, c, rph, q_off, Sq);
+    return hipGetLastError();
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
+// key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
+// partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
-                                  float *O, int Hq, int Hkv, int Sq, int Sk, float c,
-                                  hipStream_t st) {
-    const int nqt = (Sq + NW * 32 - 1) / (NW * 32);
-    const long nblk = (long)Hq * nqt;
+                                  float *O, int Hq, int Hkv, int Sq, int Sk, float c, float *pm,
+                                  float *pl, float *pacc, long slots, hipStream_t st) {
+    constexpr int BQ = NW * 32;
+    const int nqt = (Sq + BQ - 1) / BQ;
+    long nblk = (long)Hq * nqt;
+    int split_first = -1, prows = 0;
+    if (CAUSAL && pm && nqt >= 2 && nblk <= device_cus()) {
+        const int sf = nqt / 2;
+        const long pr = (long)Sq - (long)sf * BQ;
+        if (pr > 0 && 2L * Hq * pr <= slots) {
+            split_first = sf;
+            prows = (int)pr;
+            nblk = (long)Hq * (nqt + (nqt - sf));
+        }
+    }
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
-                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, c, nqt);
-    return hipGetLastError();
+                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, c, nqt, split_first, pm,
+                       pl, pacc, prows);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || split_first < 0)
+        return e;
+    return launch_merge(pm, pl, pacc, O, (long)Hq * prows, DP, 2, c, prows, split_first * BQ, Sq,
+                        st);
 }
 
 // Waves per workgroup for the fast prefill kernel: 8 (256 query rows, one workgroup per CU,
@@ -950,12 +1095,14 @@ static int prefill_waves(int Hq, int Sq) {
 
 template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                                 int Hq, int Hkv, int Sq, int Sk, float c, hipStream_t st) {
+                                 int Hq, int Hkv, int Sq, int Sk, float c, float *pm, float *pl,
+                                 float *pacc, long slots, hipStream_t st) {
     if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
         if (prefill_waves(Hq, Sq) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
-                                                                 st);
-    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+                                                                 pm, pl, pacc, slots, st);
+    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
+                                                         pacc, slots, st);
 }
 
 // The fast kernel needs D == DP, 16-byte vectors (vec; with V^T also Sk % 8 == 0, which the host
@@ -965,14 +1112,16 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
 template <int DP, int KT>
 hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                              int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                             float c, hipStream_t st) {
+                             float c, float *pm, float *pl, float *pacc, long slots,
+                             hipStream_t st) {
     constexpr int KTG = (DP == 128 && KT == 128) ? 64 : KT;
     const bool fast = vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL;
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vt != 0, [&](auto VTF) {
             constexpr bool kC = decltype(CA)::value, kT = decltype(VTF)::value;
             if (fast)
-                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, st);
+                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
+                                                             pacc, slots, st);
             return with_flag(vec != 0, [&](auto VE) {
                 return launch_prefill_t<DP, KTG, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
                                                                                Sq, Sk, D, c, st);
@@ -984,14 +1133,18 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
 template <int DP>
 hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                            int kt, float c, hipStream_t st) {
+                            int kt, float c, float *pm, float *pl, float *pacc, long slots,
+                            hipStream_t st) {
     switch (kt) {
     case 32:
-        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
+        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
+                                         pl, pacc, slots, st);
     case 64:
-        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
+        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
+                                         pl, pacc, slots, st);
     case 128:
-        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, st);
+        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
+                                          pl, pacc, slots, st);
     default:
         return hipErrorInvalidValue;
     }
@@ -1022,18 +1175,21 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
 
 // ---- extern "C" launchers called by the C host layer (attn_flash.c) -------------------------
 // vt = 1: V is V^T [Hkv][D][Sk] (pack_v_full's layout); vec must then also imply Sk % 8 == 0.
+// pm/pl/pacc: split partial slots in the caller's scratch (slots of them); NULL disables the
+// causal key split.
 extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                        float *O, int Hq, int Hkv, int Sq, int Sk, int D,
                                        int causal, int vec, int vt, int dp, int kt, float c,
+                                       float *pm, float *pl, float *pacc, long slots,
                                        void *stream) {
     hipStream_t st = (hipStream_t)stream;
     switch (dp) {
     case 64:
         return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
-                                         st);
+                                         pm, pl, pacc, slots, st);
     case 128:
         return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
-                                          st);
+                                          pm, pl, pacc, slots, st);
     default:
         return (int)hipErrorInvalidValue;
     }
@@ -1057,13 +1213,9 @@ extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, cons
 }
 
 extern "C" int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc,
-                                     float *O, int rows, int D, int nsplit, float c,
+                                     float *O, int rows, int D, int nsplit, float c, int Sq,
                                      void *stream) {
-    if (rows <= 0)
-        return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(128), 0,
-                       (hipStream_t)stream, pm, pl, pacc, O, D, nsplit, c);
-    return (int)hipGetLastError();
+    return (int)launch_merge(pm, pl, pacc, O, rows, D, nsplit, c, Sq, 0, Sq, (hipStream_t)stream);
 }
 
 extern "C" int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D,
