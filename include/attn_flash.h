@@ -13,7 +13,8 @@
  *     D outside [1, ATTN_D_MAX], a NULL or misaligned scratch, and HIP errors.
  *   - The scratch keeps the reference's contract (caller-owned, size depends only on
  *     (D, bk), monotone in bk, the kernel allocates nothing and keeps no state) but its
- *     content is the GPU's: split-K partials (m, l, acc[D]) for the decode path.
+ *     content is the GPU's: split-K partials (m, l, acc[D]), 65536 slots, for the decode
+ *     path and for causal prefills too small to fill the GPU (34 MB at D = 128).
  *
  * Layouts (row-major, bf16 stored as uint16_t bits, O fp32):
  *   Q, O [Hq][Sq][D];  K, V [Hkv][Sk][D];  V^T when v_prepacked=1: [Hkv][D][Sk].
