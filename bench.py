@@ -276,21 +276,25 @@ def main():
             for x in b[:4]:
                 x.free()
         # ---- config 3 at 1k/2k, config 4, config 5, config 1 --------------------------------
-        cases = [("c3_gqa_prefill_1k", 4, 32, 8, 1024, 1024, 128, 1.0, 3, [args.bk]),
-                 ("c3_gqa_prefill_2k", 4, 32, 8, 2048, 2048, 128, 1.0, 3, [args.bk]),
-                 ("c4_mqa_prefill_2k", 8, 16, 1, 2048, 2048, 128, 1.0, 4, [args.bk]),
-                 ("c5_ragged_gqa", 2, 24, 6, 1000, 4000, 64, 4.0, 5, [32, 64, 128, 256, 512]),
-                 ("c1_mha_256", 1, 4, 4, 256, 256, 64, 1.0, 1, [128])]
-        for name, Bc, Hqc, Hkvc, Sq, Sk, Dc, sq, ci, bks in cases:
-            fl = 4.0 * Bc * Hqc * Sq * Sk * Dc
+        # (name, B, Hq, Hkv, Sq, Sk, D, sigma_q, seed index, bks, causal); the last one is the
+        # reference's own --long case (flash.c:1312-1314), causal, useful flops only
+        cases = [("c3_gqa_prefill_1k", 4, 32, 8, 1024, 1024, 128, 1.0, 3, [args.bk], 0),
+                 ("c3_gqa_prefill_2k", 4, 32, 8, 2048, 2048, 128, 1.0, 3, [args.bk], 0),
+                 ("c4_mqa_prefill_2k", 8, 16, 1, 2048, 2048, 128, 1.0, 4, [args.bk], 0),
+                 ("c5_ragged_gqa", 2, 24, 6, 1000, 4000, 64, 4.0, 5, [32, 64, 128, 256, 512], 0),
+                 ("c1_mha_256", 1, 4, 4, 256, 256, 64, 1.0, 1, [128], 0),
+                 ("qwen3_4k_causal", 1, 16, 8, 4096, 4096, 128, 1.0, 6, [args.bk], 1)]
+        for name, Bc, Hqc, Hkvc, Sq, Sk, Dc, sq, ci, bks, cz in cases:
+            pairs = Sq * Sk if not cz else sum(min(Sk, max(0, Sk - Sq + i + 1)) for i in range(Sq))
+            fl = 4.0 * Bc * Hqc * pairs * Dc
             cb = make_inputs(ts, Bc, Hqc, Hkvc, Sq, Sk, Dc, SEED0 + ci, sigma_q=sq, copies=1)
             sc = ts.DeviceBuffer(ts.attn_flash_scratch_bytes(Dc, max(bks)))
             res = {}
             for bk in bks:
-                w, k = time_calls(ts, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, 0, bk, sc, 20, 3)
+                w, k = time_calls(ts, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, cz, bk, sc, 20, 3)
                 res["bk%d" % bk] = {"kernel_ms": k, "TFLOP_s": fl / (k * 1e-3) / 1e12,
                                     "mfma_frac": fl / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
-            res["parity"] = parity(ts, o, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, 0, 8, nthreads)
+            res["parity"] = parity(ts, o, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, cz, 8, nthreads)
             extra[name] = res
             log(name, res)
             for b in cb:
