@@ -1101,8 +1101,11 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
         if (prefill_waves(Hq, Sq) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
                                                                  pm, pl, pacc, slots, st);
-    return launch_prefill_fast_nw<DP, KT, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
-                                                         pacc, slots, st);
+    // 4-wave workgroups at D = 128 take 64-key tiles: at 128 keys the tiles use 151 KB of LDS and
+    // a CU could hold only one such workgroup (one wave per SIMD).
+    constexpr int KT4 = (DP == 128 && KT == 128) ? 64 : KT;
+    return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
+                                                          pacc, slots, st);
 }
 
 // The fast kernel needs D == DP, 16-byte vectors (vec; with V^T also Sk % 8 == 0, which the host
