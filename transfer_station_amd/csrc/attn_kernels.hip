@@ -348,15 +348,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill, fast path: D == DP (64 or 128) and 16-byte aligned tensors. Same tiling as
-// attn_prefill_kernel, plus:
+// Prefill, fast path: D == DP (64 or 128) and 16-byte aligned tensors. The MFMA tiling of
+// attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per SIMD), plus:
 //   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
 //     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
 //     offset (the range-checked one); the scalar offset is always 0.
+//   * the next 32-key sub-tile's K fragments are read from LDS between the current sub-tile's
+//     MFMAs; the row max is a max3 tree plus a VALU lane exchange (max_xor32).
 //   * lazy rescale: the running max a row subtracts is only raised when a new score exceeds it
 //     by more than kLazyLog2 (in log2 units); p is then at most 2^kLazyLog2 and the accumulator
 //     rescale (alpha != 1) runs only on those rare tiles, decided wave-uniformly. In exact
 //     arithmetic the result is identical (softmax is shift-invariant and alpha == 1 otherwise).
+//   * causal: work items are dispatched heaviest first; on grids of at most one workgroup per
+//     CU the key range of each upper-half query tile is split over two workgroups, which write
+//     partials (m, l, acc) for attn_merge2_kernel instead of O.
 // ------------------------------------------------------------------------------------------
 constexpr float kLazyLog2 = 8.0f;
 
