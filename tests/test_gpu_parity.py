@@ -360,3 +360,35 @@ def test_timing_struct_and_scratch_reuse(oracle):
             O = do.download(np.float32)
             assert oracle.cmp_rows(R, O, Hq, Sq, D, rows)[0], bk
     assert tm.qxk > 0 and tm.packv == 0 and tm.softmax == 0 and tm.sxv == 0
+
+
+# ---- tiling variants (the GPU analogue of the reference's VL sweep, README:502-508) ----------------
+_WAVES_SCRIPT = r"""
+import sys, numpy as np
+sys.path.insert(0, %r)
+import transfer_station_amd as ts
+from oracle import oracle as o
+for (Hq, Hkv, Sq, Sk, D, causal, bk) in [(32, 8, 1024, 1024, 128, 0, 128), (16, 8, 2048, 2048, 128, 1, 128),
+                                         (24, 6, 1000, 4000, 64, 0, 128), (8, 2, 700, 900, 128, 1, 64)]:
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 77)
+    O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+    rows = o.ref_rowset(Sq, 8)
+    R = o.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, rows, nthreads=8)
+    ok, mad, maxref, nbad = o.cmp_rows(R, O, Hq, Sq, D, rows)
+    print("waves case", Hq, Hkv, Sq, Sk, D, causal, bk, mad / maxref, nbad, flush=True)
+    assert ok
+print("OK")
+"""
+
+
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_forced_wave_counts(waves):
+    """Both workgroup shapes of the fast kernel (4 waves x 32 rows, 8 waves x 32 rows), forced
+    through ATTN_PREFILL_WAVES in a child process, on shapes that normally take the other."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, ATTN_PREFILL_WAVES=waves)
+    r = subprocess.run([sys.executable, "-c", _WAVES_SCRIPT % root], env=env, capture_output=True,
+                       text=True, timeout=240)
+    say(r.stdout[-2000:] + r.stderr[-2000:])
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK")
