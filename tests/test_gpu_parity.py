@@ -109,6 +109,20 @@ def test_decode_split_paths(oracle, Hkv, Sk):
     check(oracle, "decode split causal Sq=4", Q, K, V, Hq, Hkv, 4, Sk, D, 1, 128)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
+    (32, 4, 8, 1000, 128, 1),   # g*Sq = 64: four 16-row blocks (speculative decoding, GQA 8)
+    (64, 1, 1, 3000, 128, 0),   # MQA decode with 64 query heads
+    (8, 2, 5, 300, 64, 1),      # 20 rows: a partial second block
+    (6, 3, 17, 200, 40, 1),     # 34 rows, D = 40
+    (16, 2, 3, 4096, 128, 0),   # 24 rows, split over the key range
+    (4, 4, 17, 64, 64, 0),      # g = 1, Sq = 17
+])
+def test_decode_row_blocks(oracle, Hq, Hkv, Sq, Sk, D, causal):
+    """Up to 64 query rows per kv head (g*Sq) take the split-K decode kernel in 16-row blocks."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 60 + Sq)
+    check(oracle, "decode row blocks", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
+
+
 @pytest.mark.parametrize("S", [1024, 2048, 4096])
 def test_c3_gqa_prefill(oracle, S):
     B, Hq, Hkv, D = 4, 32, 8, 128
@@ -289,6 +303,8 @@ VT_CASES = [
     ("decode Sq=2 causal", 4, 1, 2, 1000, 64, 1, 128),
     ("decode Sk%8!=0", 8, 1, 2, 4099, 128, 1, 128),
     ("decode D40", 4, 2, 1, 300, 40, 0, 128),
+    ("decode 40 rows", 8, 1, 5, 999, 128, 1, 128),
+    ("decode 64 rows Sk%8!=0", 32, 4, 8, 1001, 128, 0, 128),
 ]
 
 

@@ -2,7 +2,7 @@
  *
  * Validates exactly as the reference does (bk aborts at both doors, flash.c:641-647,680,764),
  * plus the tightenings listed in include/attn_flash.h, chooses the kernel (MFMA prefill, or
- * split-K decode + merge when the g*Sq query rows of a kv head fit one 16-row MFMA tile),
+ * split-K decode + merge when a kv head has at most 64 query rows g*Sq, in 16-row blocks),
  * and launches it on the calling thread's stream. It allocates nothing per call: the decode
  * partials live in the caller's scratch, exactly as the reference's tiles do.
  */
@@ -23,7 +23,7 @@ int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t
 int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
                            int D, int causal, int vec, int vt, int dp, float c, int nsplit,
-                           int kps, void *stream);
+                           int kps, int nrb, void *stream);
 int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, float *O, int rows,
                           int D, int nsplit, float c, int Sq, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
@@ -135,14 +135,16 @@ static int attn_kt_for_bk(int bk, int dp) {
     return (bk <= 32) ? 32 : (bk == 64 ? 64 : 128);
 }
 
-#define ATTN_DECODE_ROWS 16 /* query rows per kv head the decode MFMA tile holds */
+#define ATTN_DECODE_ROWS 16     /* query rows the decode MFMA tile holds (one row block) */
+#define ATTN_DECODE_MAX_ROWS 64 /* g*Sq rows per kv head up to which decode beats prefill */
 #define ATTN_DECODE_TARGET_WG 512
 #define ATTN_DECODE_MIN_KEYS 128 /* keys per split: one 32-key tile per wave, 4 waves */
 
-static void attn_decode_split(int Hq, int Hkv, int Sq, int Sk, int *nsplit_o, int *kps_o) {
+static void attn_decode_split(int Hq, int Hkv, int Sq, int Sk, int nrb, int *nsplit_o,
+                              int *kps_o) {
     long rows = (long)Hq * Sq;
     long cap = ATTN_SLOTS / (rows > 0 ? rows : 1);
-    long want = (ATTN_DECODE_TARGET_WG + Hkv - 1) / Hkv;
+    long want = (ATTN_DECODE_TARGET_WG + (long)Hkv * nrb - 1) / ((long)Hkv * nrb);
     long by_len = (Sk + ATTN_DECODE_MIN_KEYS - 1) / ATTN_DECODE_MIN_KEYS;
     long ns = want;
     if (ns > by_len)
@@ -201,13 +203,15 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         attn_events();
         attn_hip_check(hipEventRecord(t_ev0, (hipStream_t)st), who);
     }
-    if ((long)group * Sq <= ATTN_DECODE_ROWS) {
+    if ((long)group * Sq <= ATTN_DECODE_MAX_ROWS) {
+        const int nrb = (group * Sq + ATTN_DECODE_ROWS - 1) / ATTN_DECODE_ROWS;
         int nsplit, kps;
-        attn_decode_split(Hq, Hkv, Sq, Sk, &nsplit, &kps);
+        attn_decode_split(Hq, Hkv, Sq, Sk, nrb, &nsplit, &kps);
         struct attn_carve cv;
         attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_decode(Q, K, V, O, cv.m, cv.l, cv.acc, Hq, Hkv, Sq, Sk, D,
-                                              causal ? 1 : 0, vec, vt, dp, c, nsplit, kps, st),
+                                              causal ? 1 : 0, vec, vt, dp, c, nsplit, kps, nrb,
+                                              st),
                        who);
         if (nsplit > 1)
             attn_hip_check(

@@ -682,8 +682,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Decode (split-K). One workgroup per (kv head u, split sp) serves all M = g*Sq <= 16 query
-// rows of that kv head from ONE read of its K/V range [sp*kps, min(sp*kps+kps, Sk)). Waves
+// Decode (split-K). One workgroup per (kv head u, split sp, 16-row block rb) serves up to 16 of
+// the M = g*Sq <= 64 query rows of that kv head from one read of its K/V range
+// [sp*kps, min(sp*kps+kps, Sk)) (the row blocks of a range share it through L2). Waves
 // take interleaved 32-key tiles, starting at a workgroup-dependent 128-key step; per tile
 // (v_mfma_f32_16x16x32_bf16):
 //   S^T[key][row] = K . Q^T  (A = K rows loaded from global straight into the operand layout)
@@ -698,7 +699,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
     float *__restrict__ pl, float *__restrict__ pacc, int Hq, int Hkv, int Sq, int Sk, int D,
-    float c, int nsplit, int kps) {
+    float c, int nsplit, int kps, int nrb) {
     constexpr int VSTR = DP + 16;
     constexpr int VNCH = 32 * DP / 8 / 64; // 16-byte chunks per lane per V tile
     constexpr int VTILE = 32 * VSTR;       // elements of one wave's V tile
@@ -707,14 +708,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     // The 4-wave merge reuses the V tiles' memory as float [4][16][DP].
     static_assert(4 * 16 * DP * 4 <= 4 * VTILE * 2, "merge area must fit in the V tiles");
 
+    // Block = (kv head u, split sp, row block rb): rows 16rb .. 16rb+15 of the kv head's M rows.
+    // Row blocks of one (u, sp) are consecutive logical ids, kept on one XCD so that they share
+    // its L2 copy of the K/V range.
     const int g = Hq / Hkv, M = g * Sq;
-    const int u = (int)blockIdx.x / nsplit, sp = (int)blockIdx.x % nsplit;
+    const int L = (nrb > 1) ? xcd_remap((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+    const int rb = L % nrb, us = L / nrb;
+    const int u = us / nsplit, sp = us % nsplit;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, grp = lane >> 4;
     const int k0 = sp * kps, k1 = min(k0 + kps, Sk);
+    const int row0 = 16 * rb, Mb = min(16, M - row0);
 
-    const bool rvalid = r16 < M;
-    const int gi = rvalid ? r16 / Sq : 0, qi = rvalid ? r16 % Sq : 0;
+    const bool rvalid = row0 + r16 < M;
+    const int gi = rvalid ? (row0 + r16) / Sq : 0, qi = rvalid ? (row0 + r16) % Sq : 0;
     const int h = u * g + gi;
     const uint16_t *Kh = K + (size_t)u * Sk * D;
     const uint16_t *Vh = V + (size_t)u * Sk * D;
@@ -737,7 +744,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     // then read different column ranges at the same time, which spreads a V^T input's
     // 2*Sk-byte-strided rows over more HBM channels.
     const int nsteps = (k1 - k0 + 127) / 128;
-    const int rot = (int)blockIdx.x % (nsteps > 0 ? nsteps : 1);
+    const int rot = us % (nsteps > 0 ? nsteps : 1);
     for (int js = 0; js < nsteps; ++js) {
         const int step = (js + rot < nsteps) ? js + rot : js + rot - nsteps;
         const int tb = k0 + step * 128 + w * 32;
@@ -844,7 +851,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         for (int i = 0; i < 4; ++i)
             om[(w * 16 + r16) * DP + db * 16 + 4 * grp + i] = o[db][i];
     __syncthreads();
-    for (int idx = tid; idx < M * D; idx += 256) {
+    for (int idx = tid; idx < Mb * D; idx += 256) {
         const int r = idx / D, d = idx - r * D;
         float mx = kNegInf;
 #pragma unroll
@@ -858,7 +865,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             acc += wgt * om[(ww * 16 + r) * DP + d];
             lsum += wgt * red_l[ww][r];
         }
-        const int hr = u * g + r / Sq, qr = r % Sq;
+        const int hr = u * g + (row0 + r) / Sq, qr = (row0 + r) % Sq;
         const size_t orow = (size_t)hr * Sq + qr;
         if (nsplit == 1) {
             O[orow * D + d] = acc * ((lsum > 0.f) ? 1.0f / lsum : 0.f);
@@ -1162,8 +1169,8 @@ template <int DP>
 hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
                            int D, int causal, int vec, int vt, float c, int nsplit, int kps,
-                           hipStream_t st) {
-    const long nblk = (long)Hkv * nsplit;
+                           int nrb, hipStream_t st) {
+    const long nblk = (long)Hkv * nsplit * nrb;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
     return with_flag(causal != 0, [&](auto CA) {
@@ -1172,7 +1179,7 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
                 hipLaunchKernelGGL((attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
                                                        decltype(VTF)::value>),
                                    dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl,
-                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps);
+                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
                 return hipGetLastError();
             });
         });
@@ -1203,18 +1210,20 @@ extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, con
     }
 }
 
+// nrb: 16-row blocks per kv head (g*Sq rows), one workgroup each.
 extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                       float *O, float *pm, float *pl, float *pacc, int Hq,
                                       int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                                      int dp, float c, int nsplit, int kps, void *stream) {
+                                      int dp, float c, int nsplit, int kps, int nrb,
+                                      void *stream) {
     hipStream_t st = (hipStream_t)stream;
     switch (dp) {
     case 64:
         return (int)launch_decode_d<64>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal, vec,
-                                        vt, c, nsplit, kps, st);
+                                        vt, c, nsplit, kps, nrb, st);
     case 128:
         return (int)launch_decode_d<128>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal,
-                                         vec, vt, c, nsplit, kps, st);
+                                         vec, vt, c, nsplit, kps, nrb, st);
     default:
         return (int)hipErrorInvalidValue;
     }
