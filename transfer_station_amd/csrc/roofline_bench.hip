@@ -4,6 +4,7 @@
 //
 //   roofline_bench                 all measurements, one JSON line
 //   roofline_bench mfma            bf16 MFMA peak (v_mfma_f32_32x32x16_bf16, 16x16x32_bf16)
+//   roofline_bench clock           MFMA-only rate and shader clock, constant vs random operands
 //   roofline_bench copy <MiB>      one float4 copy of <MiB> MiB (PMC calibration: known bytes)
 //   roofline_bench read <MiB>      streaming read of <MiB> MiB
 //
@@ -12,6 +13,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include <vector>
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
@@ -74,6 +77,47 @@ __global__ __launch_bounds__(256) void mfma32_peak_random(const unsigned *r, flo
     for (int i = 0; i < 16; ++i)
         s += c0[i] + c1[i] + c2[i] + c3[i];
     out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+// MFMA-only chains (as mfma32_peak / mfma32_peak_random) that also record, for wave 0 of each
+// block, the shader-clock ticks (s_memtime) and the 100 MHz real-time ticks (s_memrealtime)
+// across the loop: their ratio is the clock the chip ran at under that load.
+template <bool RANDOM>
+__global__ __launch_bounds__(256) void mfma32_clock(const unsigned *r, float *out,
+                                                   unsigned long long *clk, int iters) {
+    typedef __attribute__((ext_vector_type(4))) unsigned u4;
+    bf16x8 op[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        u4 v;
+        if (RANDOM) {
+            v = *(const u4 *)(r + ((threadIdx.x & 63) * 8 + k) * 4);
+            v = (v & 0x80FF80FFu) | 0x3E003E00u;
+        } else {
+            v = u4{0x3F803F80u, 0x40003F80u, 0x3F804000u, 0x3F803F80u};
+        }
+        op[k] = __builtin_bit_cast(bf16x8, v);
+    }
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[k], op[k + 1], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[k + 1], op[(k + 2) & 7], c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[(k + 3) & 7], op[k], c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(op[(k + 5) & 7], op[(k + 6) & 7], c3, 0, 0, 0);
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.f;
+    for (int i = 0; i < 16; ++i)
+        s += c0[i] + c1[i] + c2[i] + c3[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = s;
+    if (threadIdx.x == 0) {
+        clk[2 * blockIdx.x] = t1 - t0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
 }
 
 // One or two dependent accumulation chains per wave (how a single S^T chain is served).
@@ -295,6 +339,54 @@ static double run_mfma_random() {
     CHECK(hipFree(out));
     CHECK(hipFree(r));
     return best;
+}
+
+// TFLOP/s and the shader clock (GHz, from s_memtime over the 100 MHz s_memrealtime) of the
+// MFMA-only loop with constant or random operands.
+template <bool RANDOM> static void run_clock(double *tflops, double *ghz) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus * 8, threads = 256, iters = 5000;
+    float *out;
+    unsigned *r;
+    unsigned long long *clk;
+    CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(float)));
+    CHECK(hipMalloc(&r, 64 * 8 * 4 * sizeof(unsigned)));
+    CHECK(hipMalloc(&clk, (size_t)blocks * 2 * sizeof(unsigned long long)));
+    unsigned h[2048];
+    unsigned x = 0x12345678u;
+    for (int i = 0; i < 2048; ++i) {
+        x ^= x << 13; x ^= x >> 17; x ^= x << 5;
+        h[i] = x;
+    }
+    CHECK(hipMemcpy(r, h, sizeof h, hipMemcpyHostToDevice));
+    std::vector<unsigned long long> hc((size_t)blocks * 2);
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    *tflops = 0;
+    *ghz = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        hipLaunchKernelGGL(mfma32_clock<RANDOM>, dim3(blocks), dim3(threads), 0, 0, r, out, clk,
+                           iters);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        const double ms = time_ms(a, b);
+        const double tf = (double)blocks * (threads / 64) * iters * 16 * 32768.0 / (ms * 1e-3) / 1e12;
+        if (tf > *tflops) {
+            *tflops = tf;
+            CHECK(hipMemcpy(hc.data(), clk, hc.size() * sizeof(unsigned long long),
+                            hipMemcpyDeviceToHost));
+            double sum = 0;
+            for (int i = 0; i < blocks; ++i)
+                sum += (double)hc[2 * i] / (double)hc[2 * i + 1];
+            *ghz = sum / blocks * 0.1; // real-time counter: 100 MHz
+        }
+    }
+    CHECK(hipFree(out));
+    CHECK(hipFree(r));
+    CHECK(hipFree(clk));
 }
 
 static double run_mfma(int which) {
@@ -523,6 +615,13 @@ int main(int argc, char **argv) {
         printf("{\"mfma32x32x16_bf16_tflops\": %.1f, \"mfma16x16x32_bf16_tflops\": %.1f, "
                "\"mfma32x32x16_bf16_random_operands_tflops\": %.1f}\n",
                run_mfma(32), run_mfma(16), run_mfma_random());
+    } else if (!strcmp(mode, "clock")) {
+        double tc, gc, tr, gr;
+        run_clock<false>(&tc, &gc);
+        run_clock<true>(&tr, &gr);
+        printf("{\"mfma_const_operands_tflops\": %.1f, \"mfma_const_operands_ghz\": %.3f, "
+               "\"mfma_random_operands_tflops\": %.1f, \"mfma_random_operands_ghz\": %.3f}\n",
+               tc, gc, tr, gr);
     } else if (!strcmp(mode, "split")) {
         for (int nv = 0; nv <= 8; nv += (nv == 0 ? 4 : 2))
             printf("{\"valu_per_mfma_other_wave\": %d, \"mfma_tflops_vgpr_acc\": %.1f, "
@@ -555,7 +654,7 @@ int main(int argc, char **argv) {
                "\"copy_gbps\": %.1f, \"read_gbps\": %.1f, \"stream_mib\": %zu}\n",
                m32, m16, mr, cp, rd, mib);
     } else {
-        fprintf(stderr, "usage: %s [all|mfma|copy MiB|read MiB]\n", argv[0]);
+        fprintf(stderr, "usage: %s [all|mfma|clock|split|coissue|chain|lds|valu|copy MiB|read MiB]\n", argv[0]);
         return 2;
     }
     return 0;
