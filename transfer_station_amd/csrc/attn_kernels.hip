@@ -15,7 +15,7 @@
 //   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D == DP in {64, 128}; one
 //                                          workgroup = NW waves x 32 query rows
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 128 and alignment
-//   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 16 rows per kv head
+//   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
 //   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
 //                                          vector path / any shape)
@@ -352,7 +352,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 // attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per SIMD), plus:
 //   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
 //     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
-//     offset (the range-checked one); the scalar offset is always 0.
+//     offset (the range-checked one); the scalar offset is always 0. With row-major V they are
+//     LDS-DMA loads straight into swizzled LDS tiles (no staging registers or LDS writes); with
+//     V^T they go through registers into padded tiles.
 //   * the next 32-key sub-tile's K fragments are read from LDS between the current sub-tile's
 //     MFMAs; the row max is a max3 tree plus a VALU lane exchange (max_xor32).
 //   * lazy rescale: the running max a row subtracts is only raised when a new score exceeds it
@@ -380,6 +382,15 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// LDS-DMA: 16 bytes per lane from buffer r at byte voff + IMM straight into LDS, lane i writing
+// [lds + IMM + 16 i, +16) (the immediate offset moves both addresses; lds must be wave-uniform).
+// Bytes past the buffer's range arrive as zero. Completion is counted by vmcnt.
+template <int IMM>
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             voff, 0, IMM, 0);
+}
+
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
@@ -390,16 +401,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     constexpr int D = DP;
     constexpr int NT = NW * 64; // threads per workgroup
     constexpr int BQ = NW * 32; // query rows per workgroup
+    // Row-major V (!VT): K and V tiles arrive by LDS-DMA in swizzled, unpadded layouts (below).
+    // V^T (VT): register staging into padded tiles, K rows KSTR apart, V^T rows VTSTR apart.
     constexpr int KSTR = DP + 8;
-    // V rows are 2*VSTR bytes apart; 2*VSTR = 64 (mod 256) puts the two 16-lane groups of a
-    // transposed read (same 4 rows, columns 32 bytes apart) on disjoint LDS banks.
-    // (The D=64, 128-key tile keeps a 32-byte pad so two workgroups still fit a CU's LDS.)
-    constexpr int VSTR = (DP == 64 && KT == 128) ? DP + 16 : DP + 32;
     constexpr int VTSTR = KT + 8; // V^T tile (VT): DP rows of KT keys, 16-byte pad
     constexpr int NCH = KT * DP / 8 / NT;
     static_assert(NCH >= 1 && (KT * DP / 8) % NT == 0, "chunking");
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][VT ? DP * VTSTR : KT * VSTR];
+    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][VT ? KT * KSTR : KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][VT ? DP * VTSTR : KT * DP];
 
     const int g = Hq / Hkv;
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -476,10 +485,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
         for (int i = 0; i < 16; ++i)
             o[db][i] = 0.f;
 
-    // Tile kt's chunk r of this thread sits at byte kt*KT*D*2 + r*NT*16 + tid*16 of the head.
-    // A V^T chunk (VT) is keys [kt*KT + kc, +8) of row d: byte (d*Sk + kt*KT + kc)*2, which
-    // needs Sk % 8 == 0; a chunk past Sk would wrap into row d+1, so it gets an offset beyond
-    // the buffer's range (kvbytes < 2^31) and reads as zero.
+    // VT staging through registers. Tile kt's K chunk r of this thread sits at byte
+    // kt*KT*D*2 + r*NT*16 + tid*16 of the head. A V^T chunk is keys [kt*KT + kc, +8) of row d:
+    // byte (d*Sk + kt*KT + kc)*2, which needs Sk % 8 == 0; a chunk past Sk would wrap into row
+    // d+1, so it gets an offset beyond the buffer's range (kvbytes < 2^31) and reads as zero.
     const uint32_t voff = (uint32_t)tid * 16u;
     u32x4 kr[NCH], vr[NCH];
     auto gload = [&](int kt) {
@@ -487,14 +496,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 #pragma unroll
         for (int r = 0; r < NCH; ++r) {
             kr[r] = buf_load16(rk, base + r * (NT * 16u), 0u);
-            if (VT) {
-                const int cidx = tid + NT * r;
-                const int d = cidx / (KT / 8), key = kt * KT + (cidx % (KT / 8)) * 8;
-                const uint32_t off = (key < Sk) ? ((uint32_t)d * Sk + key) * 2u : 0x80000000u;
-                vr[r] = buf_load16(rv, off, 0u);
-            } else {
-                vr[r] = buf_load16(rv, base + r * (NT * 16u), 0u);
-            }
+            const int cidx = tid + NT * r;
+            const int d = cidx / (KT / 8), key = kt * KT + (cidx % (KT / 8)) * 8;
+            const uint32_t off = (key < Sk) ? ((uint32_t)d * Sk + key) * 2u : 0x80000000u;
+            vr[r] = buf_load16(rv, off, 0u);
         }
     };
     auto swrite = [&](int buf) {
@@ -503,13 +508,56 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
             const int cidx = tid + NT * r;
             const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
             *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
-            if (VT) {
-                const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
-                *reinterpret_cast<u32x4 *>(&Vs[buf][d * VTSTR + kc]) = vr[r];
-            } else {
-                *reinterpret_cast<u32x4 *>(&Vs[buf][row * VSTR + col]) = vr[r];
-            }
+            const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
+            *reinterpret_cast<u32x4 *>(&Vs[buf][d * VTSTR + kc]) = vr[r];
         }
+    };
+
+    // !VT: LDS-DMA staging. Byte layout of a tile for key row r and 16-byte chunk c (d/8):
+    //   K: (r/8)*16*DP + (c/2)*256 + (r%8)*32 + ((c%2) ^ ((r/8)%2))*16
+    //   V: (r/4)*8*DP + (c/4)*256 + (r%4)*64 + (c%4)*16
+    // The 16 lanes of one pass of a 16-byte K read (16 rows, one chunk) and the 32 lanes of one
+    // pass of an 8-byte transposed V read (4 rows x 64 bytes) hit distinct banks; operand steps
+    // are immediates (K: 256 B per 16 d, 16*DP*4 B per 32 keys; V: 256 B per 32 d, 8*DP*4 B per
+    // 16 keys); each 1 KB DMA block reads whole 128-byte lines. The NI blocks per tensor go to
+    // the waves in contiguous runs of PW; this lane's source offsets within a tile:
+    constexpr int NI = KT * DP / 512;
+    constexpr int PW = NI >= NW ? NI / NW : 1;
+    static_assert(PW >= 1 && PW <= 4, "DMA blocks per wave");
+    const bool dma_wave = w * PW < NI;
+    uint32_t kso[PW];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int b = (w * PW + k) * 1024 + 16 * lane;
+        const int rg = b / (16 * DP), wi = b % (16 * DP);
+        const int r = rg * 8 + (wi % 256) / 32;
+        const int cc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
+        kso[k] = (uint32_t)(r * DP * 2 + cc * 16);
+    }
+    uint32_t vso;
+    {
+        const int b = w * PW * 1024 + 16 * lane;
+        const int rgv = b / (8 * DP), wi = b % (8 * DP);
+        const int r = rgv * 4 + (wi % 256) / 64;
+        const int cc = 4 * (wi / 256) + (wi % 64) / 16;
+        vso = (uint32_t)(r * DP * 2 + cc * 16);
+    }
+    auto dma_tile = [&](int kt, int buf) {
+        if (!dma_wave)
+            return;
+        const uint32_t toff = (uint32_t)kt * KT * D * 2;
+#pragma unroll
+        for (int k = 0; k < PW; ++k)
+            dma16<0>(rk, &Ks[buf][(w * PW + k) * 512], kso[k] + toff);
+        // Successive V blocks are 1 KB apart in LDS and in global memory alike.
+        uint16_t *vd = &Vs[buf][w * PW * 512];
+        dma16<0>(rv, vd, vso + toff);
+        if constexpr (PW > 1)
+            dma16<1024>(rv, vd, vso + toff);
+        if constexpr (PW > 2)
+            dma16<2048>(rv, vd, vso + toff);
+        if constexpr (PW > 3)
+            dma16<3072>(rv, vd, vso + toff);
     };
 
     const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
@@ -518,23 +566,43 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     // Key tiles [kt0, kt1) of this item: all of them, or one half of a split tile's range.
     const int kt0 = (part == 1) ? nkt / 2 : 0;
     const int kt1 = (part == 0) ? nkt / 2 : nkt;
+    // Fragment offsets (elements) of this lane in a DMA-staged tile: K row t*32 + kperm,
+    // chunk 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
+    const int kfo = VT ? kperm * KSTR + hi * 8
+                       : (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
+    constexpr int KSUB = VT ? 32 * KSTR : 32 * DP; // 32-key sub-tile step
+    constexpr int KDK = VT ? 16 : 128;            // 16-d step
+    const int vfo = hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
+                    (i16 & 1) * 4;
+
     if (kt0 < kt1) {
-        gload(kt0);
-        swrite(0);
+        if (VT) {
+            gload(kt0);
+            swrite(0);
+        } else {
+            dma_tile(kt0, 0);
+        }
     }
+    if (!VT)
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's DMA blocks have landed
     __syncthreads();
     for (int kt = kt0; kt < kt1; ++kt) {
         const int buf = (kt - kt0) & 1;
-        if (kt + 1 < kt1)
-            gload(kt + 1);
+        if (kt + 1 < kt1) {
+            // The other buffer's last readers finished before the barrier that ended tile kt-1.
+            if (VT)
+                gload(kt + 1);
+            else
+                dma_tile(kt + 1, buf ^ 1);
+        }
         const int kbase = kt * KT;
         if (kbase <= wave_maxkey) {
             f32x16 s[KT / 32];
-            const uint16_t *kb0 = &Ks[buf][kperm * KSTR + hi * 8];
+            const uint16_t *kb0 = &Ks[buf][kfo];
             bf16x8 ka[2][DP / 16];
 #pragma unroll
             for (int kk = 0; kk < DP / 16; ++kk)
-                ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * 16));
+                ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
             __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t) {
@@ -547,7 +615,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                     s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
                     if (t + 1 < KT / 32)
                         ka[(t + 1) & 1][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
-                            kb0 + (t + 1) * 32 * KSTR + kk * 16));
+                            kb0 + (t + 1) * KSUB + kk * KDK));
                 }
 #pragma unroll
                 for (int kk = 0; kk < DP / 16; ++kk) {
@@ -628,19 +696,20 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
                     }
                 } else {
-                    const uint16_t *vb = &Vs[buf][(cc * 16 + 8 * hi + (i16 >> 2)) * VSTR +
-                                                  (g16 & 1) * 16 + 4 * (i16 & 3)];
+                    const uint16_t *vb = &Vs[buf][vfo + cc * 16 * DP];
 #pragma unroll
                     for (int db = 0; db < DP / 32; ++db) {
-                        const bf16x8 a = join_tr(lds_read_tr(vb + db * 32),
-                                                 lds_read_tr(vb + db * 32 + 4 * VSTR));
+                        const bf16x8 a = join_tr(lds_read_tr(vb + db * 128),
+                                                 lds_read_tr(vb + db * 128 + 4 * DP));
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
                     }
                 }
             }
         }
-        if (kt + 1 < kt1)
+        if (VT && kt + 1 < kt1)
             swrite(buf ^ 1);
+        if (!VT)
+            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
         __syncthreads();
     }
 
@@ -1113,8 +1182,8 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
         if (prefill_waves(Hq, Sq) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
                                                                  pm, pl, pacc, slots, st);
-    // 4-wave workgroups at D = 128 take 64-key tiles: at 128 keys the tiles use 151 KB of LDS and
-    // a CU could hold only one such workgroup (one wave per SIMD).
+    // 4-wave workgroups at D = 128 take 64-key tiles: at 128 keys the tiles use 128-136 KB of
+    // LDS and a CU could hold only one such workgroup (one wave per SIMD).
     constexpr int KT4 = (DP == 128 && KT == 128) ? 64 : KT;
     return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
                                                           pacc, slots, st);
