@@ -352,9 +352,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 // attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per SIMD), plus:
 //   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
 //     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
-//     offset (the range-checked one); the scalar offset is always 0. With row-major V they are
-//     LDS-DMA loads straight into swizzled LDS tiles (no staging registers or LDS writes); with
-//     V^T they go through registers into padded tiles.
+//     offset (the range-checked one); the scalar offset is always 0. They are LDS-DMA loads
+//     straight into swizzled LDS tiles (no staging registers or LDS writes).
 //   * the next 32-key sub-tile's K fragments are read from LDS between the current sub-tile's
 //     MFMAs; the row max is a max3 tree plus a VALU lane exchange (max_xor32).
 //   * lazy rescale: the running max a row subtracts is only raised when a new score exceeds it
@@ -378,10 +377,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
                                              0x00020000);
 }
 
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
 // LDS-DMA: 16 bytes per lane from buffer r at byte voff + IMM straight into LDS, lane i writing
 // [lds + IMM + 16 i, +16) (the immediate offset moves both addresses; lds must be wave-uniform).
 // Bytes past the buffer's range arrive as zero. Completion is counted by vmcnt.
@@ -399,16 +394,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     float *__restrict__ pacc, int prows) {
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int D = DP;
-    constexpr int NT = NW * 64; // threads per workgroup
     constexpr int BQ = NW * 32; // query rows per workgroup
-    // Row-major V (!VT): K and V tiles arrive by LDS-DMA in swizzled, unpadded layouts (below).
-    // V^T (VT): register staging into padded tiles, K rows KSTR apart, V^T rows VTSTR apart.
-    constexpr int KSTR = DP + 8;
-    constexpr int VTSTR = KT + 8; // V^T tile (VT): DP rows of KT keys, 16-byte pad
-    constexpr int NCH = KT * DP / 8 / NT;
-    static_assert(NCH >= 1 && (KT * DP / 8) % NT == 0, "chunking");
-    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][VT ? KT * KSTR : KT * DP];
-    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][VT ? DP * VTSTR : KT * DP];
+    // K and V (or V^T) tiles arrive by LDS-DMA in swizzled, unpadded layouts (below).
+    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
 
     const int g = Hq / Hkv;
     const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -485,42 +474,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
         for (int i = 0; i < 16; ++i)
             o[db][i] = 0.f;
 
-    // VT staging through registers. Tile kt's K chunk r of this thread sits at byte
-    // kt*KT*D*2 + r*NT*16 + tid*16 of the head. A V^T chunk is keys [kt*KT + kc, +8) of row d:
-    // byte (d*Sk + kt*KT + kc)*2, which needs Sk % 8 == 0; a chunk past Sk would wrap into row
-    // d+1, so it gets an offset beyond the buffer's range (kvbytes < 2^31) and reads as zero.
-    const uint32_t voff = (uint32_t)tid * 16u;
-    u32x4 kr[NCH], vr[NCH];
-    auto gload = [&](int kt) {
-        const uint32_t base = (uint32_t)kt * KT * D * 2 + voff;
-#pragma unroll
-        for (int r = 0; r < NCH; ++r) {
-            kr[r] = buf_load16(rk, base + r * (NT * 16u), 0u);
-            const int cidx = tid + NT * r;
-            const int d = cidx / (KT / 8), key = kt * KT + (cidx % (KT / 8)) * 8;
-            const uint32_t off = (key < Sk) ? ((uint32_t)d * Sk + key) * 2u : 0x80000000u;
-            vr[r] = buf_load16(rv, off, 0u);
-        }
-    };
-    auto swrite = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < NCH; ++r) {
-            const int cidx = tid + NT * r;
-            const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-            *reinterpret_cast<u32x4 *>(&Ks[buf][row * KSTR + col]) = kr[r];
-            const int d = cidx / (KT / 8), kc = (cidx % (KT / 8)) * 8;
-            *reinterpret_cast<u32x4 *>(&Vs[buf][d * VTSTR + kc]) = vr[r];
-        }
-    };
-
-    // !VT: LDS-DMA staging. Byte layout of a tile for key row r and 16-byte chunk c (d/8):
-    //   K: (r/8)*16*DP + (c/2)*256 + (r%8)*32 + ((c%2) ^ ((r/8)%2))*16
-    //   V: (r/4)*8*DP + (c/4)*256 + (r%4)*64 + (c%4)*16
-    // The 16 lanes of one pass of a 16-byte K read (16 rows, one chunk) and the 32 lanes of one
-    // pass of an 8-byte transposed V read (4 rows x 64 bytes) hit distinct banks; operand steps
-    // are immediates (K: 256 B per 16 d, 16*DP*4 B per 32 keys; V: 256 B per 32 d, 8*DP*4 B per
-    // 16 keys); each 1 KB DMA block reads whole 128-byte lines. The NI blocks per tensor go to
-    // the waves in contiguous runs of PW; this lane's source offsets within a tile:
+    // LDS-DMA staging. Byte layout of a tile for key row r and 16-byte chunk c (d/8), and of a
+    // V^T tile for d row e and 16-byte key chunk k (8 keys):
+    //   K:   (r/8)*16*DP + (c/2)*256 + (r%8)*32 + ((c%2) ^ ((r/8)%2))*16
+    //   V:   (r/4)*8*DP + (c/4)*256 + (r%4)*64 + (c%4)*16
+    //   V^T: (e/8)*16*KT + (k/2)*256 + (e%8)*32 + ((k%2) ^ ((e/8)%2))*16
+    // The 16 lanes of one pass of a 16-byte K or V^T read (16 rows, one chunk) and the 32 lanes
+    // of one pass of an 8-byte transposed V read (4 rows x 64 bytes) hit distinct banks; operand
+    // steps are immediates (K: 256 B per 16 d, 16*DP*4 B per 32 keys; V: 256 B per 32 d,
+    // 8*DP*4 B per 16 keys; V^T: 256 B per 16 keys, 16*KT*4 B per 32 d); each 1 KB DMA block
+    // reads whole 128-byte lines of K and V, or 128-byte runs of V^T rows. The NI blocks per
+    // tensor go to the waves in contiguous runs of PW; this lane's source offsets within a tile:
     constexpr int NI = KT * DP / 512;
     constexpr int PW = NI >= NW ? NI / NW : 1;
     static_assert(PW >= 1 && PW <= 4, "DMA blocks per wave");
@@ -542,6 +506,20 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
         const int cc = 4 * (wi / 256) + (wi % 64) / 16;
         vso = (uint32_t)(r * DP * 2 + cc * 16);
     }
+    // V^T: byte d*Sk*2 + (key chunk)*16 of the head for tile 0, and the chunk's first key. A
+    // chunk at or past Sk (Sk % 8 == 0, so chunks never straddle it) would read the next d row:
+    // it gets an offset beyond the buffer's range and arrives as zero.
+    uint32_t vto[PW];
+    int vtk[PW];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int b = (w * PW + k) * 1024 + 16 * lane;
+        const int rg = b / (16 * KT), wi = b % (16 * KT);
+        const int e = rg * 8 + (wi % 256) / 32;
+        const int kc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
+        vto[k] = (uint32_t)e * (uint32_t)Sk * 2u + (uint32_t)kc * 16u;
+        vtk[k] = kc * 8;
+    }
     auto dma_tile = [&](int kt, int buf) {
         if (!dma_wave)
             return;
@@ -549,15 +527,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 #pragma unroll
         for (int k = 0; k < PW; ++k)
             dma16<0>(rk, &Ks[buf][(w * PW + k) * 512], kso[k] + toff);
-        // Successive V blocks are 1 KB apart in LDS and in global memory alike.
-        uint16_t *vd = &Vs[buf][w * PW * 512];
-        dma16<0>(rv, vd, vso + toff);
-        if constexpr (PW > 1)
-            dma16<1024>(rv, vd, vso + toff);
-        if constexpr (PW > 2)
-            dma16<2048>(rv, vd, vso + toff);
-        if constexpr (PW > 3)
-            dma16<3072>(rv, vd, vso + toff);
+        if constexpr (VT) {
+            const int klim = Sk - kt * KT; // keys of this tile that exist
+#pragma unroll
+            for (int k = 0; k < PW; ++k)
+                dma16<0>(rv, &Vs[buf][(w * PW + k) * 512],
+                         vtk[k] < klim ? vto[k] + (uint32_t)kt * KT * 2 : 0x80000000u);
+        } else {
+            // Successive V blocks are 1 KB apart in LDS and in global memory alike.
+            uint16_t *vd = &Vs[buf][w * PW * 512];
+            dma16<0>(rv, vd, vso + toff);
+            if constexpr (PW > 1)
+                dma16<1024>(rv, vd, vso + toff);
+            if constexpr (PW > 2)
+                dma16<2048>(rv, vd, vso + toff);
+            if constexpr (PW > 3)
+                dma16<3072>(rv, vd, vso + toff);
+        }
     };
 
     const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
@@ -568,33 +554,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const int kt1 = (part == 0) ? nkt / 2 : nkt;
     // Fragment offsets (elements) of this lane in a DMA-staged tile: K row t*32 + kperm,
     // chunk 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
-    const int kfo = VT ? kperm * KSTR + hi * 8
-                       : (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
-    constexpr int KSUB = VT ? 32 * KSTR : 32 * DP; // 32-key sub-tile step
-    constexpr int KDK = VT ? 16 : 128;            // 16-d step
-    const int vfo = hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
-                    (i16 & 1) * 4;
+    const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
+    constexpr int KSUB = 32 * DP; // 32-key sub-tile step
+    constexpr int KDK = 128;      // 16-d step
+    // V^T operand: d row db*32 + l32, keys cc*16 + 8hi .. +8.
+    const int vfo = VT ? (l32 >> 3) * 8 * KT + (l32 & 7) * 16 + ((hi ^ ((l32 >> 3) & 1)) * 8)
+                       : hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
+                             (i16 & 1) * 4;
 
-    if (kt0 < kt1) {
-        if (VT) {
-            gload(kt0);
-            swrite(0);
-        } else {
-            dma_tile(kt0, 0);
-        }
-    }
-    if (!VT)
-        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's DMA blocks have landed
+    if (kt0 < kt1)
+        dma_tile(kt0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's DMA blocks have landed
     __syncthreads();
     for (int kt = kt0; kt < kt1; ++kt) {
         const int buf = (kt - kt0) & 1;
-        if (kt + 1 < kt1) {
-            // The other buffer's last readers finished before the barrier that ended tile kt-1.
-            if (VT)
-                gload(kt + 1);
-            else
-                dma_tile(kt + 1, buf ^ 1);
-        }
+        // The other buffer's last readers finished before the barrier that ended tile kt-1.
+        if (kt + 1 < kt1)
+            dma_tile(kt + 1, buf ^ 1);
         const int kbase = kt * KT;
         if (kbase <= wave_maxkey) {
             f32x16 s[KT / 32];
@@ -688,11 +664,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
 #pragma unroll
             for (int cc = 0; cc < KT / 16; ++cc) {
                 if (VT) {
-                    const uint16_t *vb = &Vs[buf][l32 * VTSTR + cc * 16 + 8 * hi];
+                    const uint16_t *vb = &Vs[buf][vfo + cc * 128];
 #pragma unroll
                     for (int db = 0; db < DP / 32; ++db) {
                         const bf16x8 a =
-                            as_bf16x8(*reinterpret_cast<const u32x4 *>(vb + db * 32 * VTSTR));
+                            as_bf16x8(*reinterpret_cast<const u32x4 *>(vb + db * 32 * KT));
                         o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
                     }
                 } else {
@@ -706,10 +682,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                 }
             }
         }
-        if (VT && kt + 1 < kt1)
-            swrite(buf ^ 1);
-        if (!VT)
-            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
         __syncthreads();
     }
 
