@@ -105,6 +105,14 @@ __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t *p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) as one v_max3_f32 (the kernels run with IEEE mode off, so no NaN quieting).
+// Written as asm: from fmaxf chains the compiler splits about half of the max3s into two v_max.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // max(x[lane], x[lane ^ 32]) in the VALU: v_permlane32_swap exchanges the upper 32 lanes of its
 // first operand with the lower 32 lanes of its second, so with both operands holding x each lane
 // ends with its partner's value in one of the two; no LDS round trip (ds_bpermute) is involved.
@@ -435,15 +443,15 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     }
     const int u = h / g; // kv head
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
     const int l32 = lane & 31, hi = lane >> 5;
     const int q0 = qt * BQ + w * 32;
     const int myq = q0 + l32;
 
     const uint16_t *Qh = Q + (size_t)h * Sq * D;
     const uint32_t kvbytes = (uint32_t)Sk * D * 2;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K + (size_t)u * Sk * D, kvbytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V + (size_t)u * Sk * D, kvbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V + (size_t)u * Sk * D, kvbytes); // V^T path
 
     bf16x8 qb[DP / 16];
 #pragma unroll
@@ -523,10 +531,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     auto dma_tile = [&](int kt, int buf) {
         if (!dma_wave)
             return;
+        // Row-major K and V: descriptors based at the tile (scalar work), whose range still ends
+        // at the head's last byte, so the per-lane offsets stay loop-invariant.
         const uint32_t toff = (uint32_t)kt * KT * D * 2;
+        const __amdgpu_buffer_rsrc_t rkt = make_rsrc(K + (size_t)u * Sk * D + (size_t)kt * KT * D,
+                                                     kvbytes - toff);
 #pragma unroll
         for (int k = 0; k < PW; ++k)
-            dma16<0>(rk, &Ks[buf][(w * PW + k) * 512], kso[k] + toff);
+            dma16<0>(rkt, &Ks[buf][(w * PW + k) * 512], kso[k]);
         if constexpr (VT) {
             const int klim = Sk - kt * KT; // keys of this tile that exist
 #pragma unroll
@@ -535,14 +547,16 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                          vtk[k] < klim ? vto[k] + (uint32_t)kt * KT * 2 : 0x80000000u);
         } else {
             // Successive V blocks are 1 KB apart in LDS and in global memory alike.
+            const __amdgpu_buffer_rsrc_t rvt =
+                make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D, kvbytes - toff);
             uint16_t *vd = &Vs[buf][w * PW * 512];
-            dma16<0>(rv, vd, vso + toff);
+            dma16<0>(rvt, vd, vso);
             if constexpr (PW > 1)
-                dma16<1024>(rv, vd, vso + toff);
+                dma16<1024>(rvt, vd, vso);
             if constexpr (PW > 2)
-                dma16<2048>(rv, vd, vso + toff);
+                dma16<2048>(rvt, vd, vso);
             if constexpr (PW > 3)
-                dma16<3072>(rv, vd, vso + toff);
+                dma16<3072>(rvt, vd, vso);
         }
     };
 
@@ -610,26 +624,23 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                             s[t][i] = kNegInf;
                     }
             }
-            // Row max of the tile as a shallow tree (independent max3 leaves, then a combine),
-            // the partner half-row through the VALU exchange, then the wave-uniform lazy-rescale
-            // test; the exponentials and the P.V MFMAs follow in one branch-free block.
-            // Independent chains of 8 scores (max3, max3, max3, max: two new values per
-            // instruction), combined at the end.
-            float mt[KT / 16];
+            // Row max of the tile: one max3 chain per 32-key sub-tile (two new scores per
+            // instruction), the chains combined, the partner half-row through the VALU exchange,
+            // then the wave-uniform lazy-rescale test; the exponentials and the P.V MFMAs follow
+            // in one branch-free block.
+            float mt[KT / 32];
 #pragma unroll
-            for (int t = 0; t < KT / 32; ++t)
+            for (int t = 0; t < KT / 32; ++t) {
+                float m = max3f(s[t][0], s[t][1], s[t][2]);
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int b = 8 * hh;
-                    float m = fmaxf(s[t][b], fmaxf(s[t][b + 1], s[t][b + 2]));
-                    m = fmaxf(m, fmaxf(s[t][b + 3], s[t][b + 4]));
-                    m = fmaxf(m, fmaxf(s[t][b + 5], s[t][b + 6]));
-                    mt[2 * t + hh] = fmaxf(m, s[t][b + 7]);
-                }
+                for (int i = 3; i < 15; i += 2)
+                    m = max3f(m, s[t][i], s[t][i + 1]);
+                mt[t] = fmaxf(m, s[t][15]);
+            }
             float mx = mt[0];
 #pragma unroll
-            for (int j = 1; j < KT / 16; j += 2)
-                mx = (j + 1 < KT / 16) ? fmaxf(mx, fmaxf(mt[j], mt[j + 1])) : fmaxf(mx, mt[j]);
+            for (int j = 1; j < KT / 32; j += 2)
+                mx = (j + 1 < KT / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
             mx = max_xor32(mx);
             const bool raise = mx > m_run + lazy_raw;
             if (__builtin_amdgcn_ballot_w64(raise) != 0) {
