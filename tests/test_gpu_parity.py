@@ -408,3 +408,41 @@ def test_forced_wave_counts(waves):
                        text=True, timeout=240)
     say(r.stdout[-2000:] + r.stderr[-2000:])
     assert r.returncode == 0 and r.stdout.strip().endswith("OK")
+
+
+# ---- seeded random shapes over every kernel and staging path ---------------------------------
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice([64, 128, 64, 128, 32, 80, 96]))
+        Hkv = int(rng.integers(1, 4))
+        g = int(rng.choice([1, 2, 4, 8, 16]))
+        Sq = int(rng.choice([1, 2, 3, 7])) if rng.random() < 0.35 else int(rng.integers(8, 700))
+        Sk = int(rng.integers(1, 1500))
+        if rng.random() < 0.5:
+            Sk = max(8, Sk - Sk % 8)  # V^T inputs take the fast kernel only when Sk % 8 == 0
+        causal = int(rng.random() < 0.5)
+        bk = int(rng.choice([16, 32, 64, 128, 256, 512]))
+        vt = int(rng.random() < 0.3)
+        cases.append((i, g * Hkv, Hkv, Sq, Sk, D, causal, bk, vt))
+    return cases
+
+
+RANDOM_CASES = _random_cases(40, 0x5EED)
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=["r%02d" % c[0] for c in RANDOM_CASES])
+def test_random_shapes(oracle, case):
+    """Seeded random shapes (GQA group 1-16, Sq 1-700, Sk 1-1500 with and without Sk % 8,
+    D in {32, 64, 80, 96, 128}, causal or not, bk 16-512, row-major V or V^T) against the
+    oracle: decode, prefill fast and general kernels, tails and the causal key split."""
+    i, Hq, Hkv, Sq, Sk, D, causal, bk, vt = case
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 1000 + i)
+    if vt:
+        vt_host = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
+        O = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=1)
+    else:
+        O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+    check(oracle, "random %d%s" % (i, " V^T" if vt else ""), Q, K, V, Hq, Hkv, Sq, Sk, D, causal,
+          bk, ref_cap=8, O=O)
