@@ -1144,10 +1144,12 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 }
 
 // Waves per workgroup for the fast prefill kernel: 8 (256 query rows, one workgroup per CU,
-// two waves per SIMD), or 4 (128 rows) when 256-row tiles would leave most CUs without a
-// workgroup (fewer than 64 of them: measured 9.1 -> 6.8 us on 4 heads x 256 rows).
+// two waves per SIMD), or 4 (128 rows; two workgroups fit a CU) when 256-row tiles would leave
+// CUs idle: at most half as many 8-wave workgroups as CUs, or for causal grids (uneven tiles)
+// at most one per CU. Measured against 8 waves: 16 heads at 2k +21%, Qwen3 causal 1k / 2k / 4k
+// +18% / +9% / +7.5%, config 5 causal +24%; above those sizes 8 waves win by 5-9%.
 // ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
-static int prefill_waves(int Hq, int Sq) {
+static int prefill_waves(int Hq, int Sq, bool causal) {
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
@@ -1155,7 +1157,8 @@ static int prefill_waves(int Hq, int Sq) {
     }
     if (forced)
         return forced;
-    return ((long)Hq * ((Sq + 255) / 256) < 64) ? 4 : 8;
+    const long n8 = (long)Hq * ((Sq + 255) / 256);
+    return (n8 <= (causal ? device_cus() : device_cus() / 2)) ? 4 : 8;
 }
 
 template <int DP, int KT, bool CAUSAL, bool VT>
@@ -1163,7 +1166,7 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                  int Hq, int Hkv, int Sq, int Sk, float c, float *pm, float *pl,
                                  float *pacc, long slots, hipStream_t st) {
     if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
-        if (prefill_waves(Hq, Sq) == 8)
+        if (prefill_waves(Hq, Sq, CAUSAL) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
                                                                  pm, pl, pacc, slots, st);
     // 4-wave workgroups at D = 128 take 64-key tiles: at 128 keys the tiles use 128-136 KB of
