@@ -156,8 +156,10 @@ def test_qwen3_causal_long(oracle):
     (16, 8, 2048, 2048, 128, 8),
     (8, 2, 1000, 3000, 128, 0),    # Sk > Sq, every row
     (4, 4, 700, 300, 64, 0),       # Sq > Sk: rows below Sq - Sk attend nothing
-    (6, 3, 600, 600, 40, 0),       # general kernel (D = 40): no split, same answer
-], ids=["qwen3-4k", "qwen3-2k", "sk>sq", "sq>sk", "d40"])
+    (6, 3, 600, 600, 40, 0),       # D = 40 on the 64-wide tiles (zero columns 40..63)
+    (8, 4, 1500, 1500, 96, 8),     # D = 96 on the 96-wide tiles
+    (8, 2, 900, 1100, 80, 8),      # D = 80 on the 96-wide tiles
+], ids=["qwen3-4k", "qwen3-2k", "sk>sq", "sq>sk", "d40", "d96", "d80"])
 def test_causal_split_small_grid(oracle, shape):
     Hq, Hkv, Sq, Sk, D, cap = shape
     Q, K, V = ts.synth_lcg_qkv(Hq, Hkv, Sq, Sk, D)
@@ -169,12 +171,12 @@ def test_causal_split_small_grid(oracle, shape):
 
 
 # ---- tails, head_dim, masks -----------------------------------------------------------------------
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("causal", [0, 1])
 @pytest.mark.parametrize("bk", [32, 64, 128])
 def test_tail_probe(oracle, bk, causal, D):
-    """The reference's tail probe (README:550-554): Sk around multiples of bk, both head sizes
-    the fast kernel is built for."""
+    """The reference's tail probe (README:550-554): Sk around multiples of bk, at each tile
+    width the fast kernel is built for."""
     for Sk in (1, bk - 1, bk, bk + 1, 2 * bk, 2 * bk + 1, 70):
         for Sq in (40, 1):
             Q, K, V = ts.synth_lcg_qkv(4, 2, Sq, Sk, D)
@@ -285,9 +287,9 @@ def test_pack_v_full_transposes_exactly(Hkv, Sk, D, offset):
 # ---- v_prepacked = 1: V^T [Hkv][D][Sk] input (flash.c:751-753,770,812-833) -----------------------
 # The reference changes only V's stride when V is pre-packed, so the math is identical. Here the
 # V^T operand of the P.V MFMA holds the same values in the same positions either way, so O is
-# bit-identical whenever both layouts run the same kernel. They do not when D is 64 or 128 and
-# Sk % 8 != 0 (a V^T row is then not 16-byte aligned and the prefill takes the general kernel):
-# those cases are held to the oracle tolerance only.
+# bit-identical whenever both layouts run the same kernel. They do not when D % 8 == 0 and
+# Sk % 8 != 0 (a V^T row is then not 16-byte aligned and the prefill takes the general kernel
+# while row-major V takes the fast one): those cases are held to the oracle tolerance only.
 VT_CASES = [
     # name, Hq, Hkv, Sq, Sk, D, causal, bk
     ("fast D128 partial tile", 8, 2, 300, 1000, 128, 0, 128),
@@ -295,7 +297,10 @@ VT_CASES = [
     ("fast D128 kt128 causal", 8, 2, 700, 1000, 128, 1, 128),
     ("fast D64 kt128 causal", 4, 4, 257, 520, 64, 1, 256),
     ("fast D64 kt32 Sk<KT", 4, 2, 100, 24, 64, 0, 16),
-    ("general D40 causal", 6, 3, 130, 70, 40, 1, 128),
+    ("D40 causal Sk%8!=0", 6, 3, 130, 70, 40, 1, 128),
+    ("fast D96 causal", 8, 2, 300, 640, 96, 1, 128),
+    ("fast D80 kt64", 8, 4, 200, 512, 80, 0, 64),
+    ("fast D40 kt32", 6, 3, 130, 72, 40, 1, 32),
     ("general D128 Sk%8!=0", 8, 2, 200, 333, 128, 0, 128),
     ("general D64 Sk%8!=0 causal", 4, 1, 64, 77, 64, 1, 32),
     ("general D7", 4, 2, 40, 50, 7, 0, 64),
@@ -318,7 +323,7 @@ def test_v_prepacked(oracle, case):
     direct = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=1)
     assert np.array_equal(packed.view(np.uint32), direct.view(np.uint32))
     decode = (Hq // Hkv) * Sq <= 64
-    same_kernel = decode or D not in (64, 128) or Sk % 8 == 0
+    same_kernel = decode or D % 8 != 0 or Sk % 8 == 0
     if same_kernel:
         nd = int(np.count_nonzero(packed.view(np.uint32) != base.view(np.uint32)))
         say("   v_prepacked vs row-major: %d differing outputs" % nd)

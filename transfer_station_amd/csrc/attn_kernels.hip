@@ -12,8 +12,8 @@
 // products s, p = 2^(s*c - m*c) equals e^(scale*s - scale*m).
 //
 // Kernels:
-//   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D == DP in {64, 128}; one
-//                                          workgroup = NW waves x 32 query rows
+//   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D % 8 == 0, D <= DP in
+//                                          {64, 96, 128}; one workgroup = NW waves x 32 rows
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 128 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
@@ -397,11 +397,11 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, u
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
-    const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk,
+    const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
     float *__restrict__ pacc, int prows) {
+    // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
-    constexpr int D = DP;
     constexpr int BQ = NW * 32; // query rows per workgroup
     // K and V (or V^T) tiles arrive by LDS-DMA in swizzled, unpadded layouts (below).
     __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
@@ -493,26 +493,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     // 8*DP*4 B per 16 keys; V^T: 256 B per 16 keys, 16*KT*4 B per 32 d); each 1 KB DMA block
     // reads whole 128-byte lines of K and V, or 128-byte runs of V^T rows. The NI blocks per
     // tensor go to the waves in contiguous runs of PW; this lane's source offsets within a tile:
+    // A chunk of columns D and beyond gets an offset past the buffer's range and arrives as zero.
     constexpr int NI = KT * DP / 512;
-    constexpr int PW = NI >= NW ? NI / NW : 1;
+    constexpr int PW = (NI + NW - 1) / NW;
     static_assert(PW >= 1 && PW <= 4, "DMA blocks per wave");
-    const bool dma_wave = w * PW < NI;
-    uint32_t kso[PW];
+    const int nblk_w = max(0, min(PW, NI - w * PW)); // this wave's blocks (wave-uniform)
+    uint32_t kso[PW], vso[PW];
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
         const int b = (w * PW + k) * 1024 + 16 * lane;
-        const int rg = b / (16 * DP), wi = b % (16 * DP);
-        const int r = rg * 8 + (wi % 256) / 32;
-        const int cc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
-        kso[k] = (uint32_t)(r * DP * 2 + cc * 16);
-    }
-    uint32_t vso;
-    {
-        const int b = w * PW * 1024 + 16 * lane;
-        const int rgv = b / (8 * DP), wi = b % (8 * DP);
-        const int r = rgv * 4 + (wi % 256) / 64;
-        const int cc = 4 * (wi / 256) + (wi % 64) / 16;
-        vso = (uint32_t)(r * DP * 2 + cc * 16);
+        {
+            const int rg = b / (16 * DP), wi = b % (16 * DP);
+            const int r = rg * 8 + (wi % 256) / 32;
+            const int cc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
+            kso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
+        }
+        {
+            const int rgv = b / (8 * DP), wi = b % (8 * DP);
+            const int r = rgv * 4 + (wi % 256) / 64;
+            const int cc = 4 * (wi / 256) + (wi % 64) / 16;
+            vso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
+        }
     }
     // V^T: byte d*Sk*2 + (key chunk)*16 of the head for tile 0, and the chunk's first key. A
     // chunk at or past Sk (Sk % 8 == 0, so chunks never straddle it) would read the next d row:
@@ -526,11 +527,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
         const int e = rg * 8 + (wi % 256) / 32;
         const int kc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
         vto[k] = (uint32_t)e * (uint32_t)Sk * 2u + (uint32_t)kc * 16u;
-        vtk[k] = kc * 8;
+        vtk[k] = (e < D) ? kc * 8 : 0x7fffffff; // d rows past D: never in range
     }
     auto dma_tile = [&](int kt, int buf) {
-        if (!dma_wave)
-            return;
         // Row-major K and V: descriptors based at the tile (scalar work), whose range still ends
         // at the head's last byte, so the per-lane offsets stay loop-invariant.
         const uint32_t toff = (uint32_t)kt * KT * D * 2;
@@ -538,25 +537,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                                                      kvbytes - toff);
 #pragma unroll
         for (int k = 0; k < PW; ++k)
-            dma16<0>(rkt, &Ks[buf][(w * PW + k) * 512], kso[k]);
+            if (NI % NW == 0 || k < nblk_w)
+                dma16<0>(rkt, &Ks[buf][(w * PW + k) * 512], kso[k]);
         if constexpr (VT) {
             const int klim = Sk - kt * KT; // keys of this tile that exist
 #pragma unroll
             for (int k = 0; k < PW; ++k)
-                dma16<0>(rv, &Vs[buf][(w * PW + k) * 512],
-                         vtk[k] < klim ? vto[k] + (uint32_t)kt * KT * 2 : 0x80000000u);
+                if (NI % NW == 0 || k < nblk_w)
+                    dma16<0>(rv, &Vs[buf][(w * PW + k) * 512],
+                             vtk[k] < klim ? vto[k] + (uint32_t)kt * KT * 2 : 0x80000000u);
         } else {
-            // Successive V blocks are 1 KB apart in LDS and in global memory alike.
             const __amdgpu_buffer_rsrc_t rvt =
                 make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D, kvbytes - toff);
-            uint16_t *vd = &Vs[buf][w * PW * 512];
-            dma16<0>(rvt, vd, vso);
-            if constexpr (PW > 1)
-                dma16<1024>(rvt, vd, vso);
-            if constexpr (PW > 2)
-                dma16<2048>(rvt, vd, vso);
-            if constexpr (PW > 3)
-                dma16<3072>(rvt, vd, vso);
+#pragma unroll
+            for (int k = 0; k < PW; ++k)
+                if (NI % NW == 0 || k < nblk_w)
+                    dma16<0>(rvt, &Vs[buf][(w * PW + k) * 512], vso[k]);
         }
     };
 
@@ -714,7 +710,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                 for (int i4 = 0; i4 < 4; ++i4) {
                     const int d = db * 32 + i4 * 8 + 4 * hi;
                     f32x4 v = {o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2], o[db][4 * i4 + 3]};
-                    *reinterpret_cast<f32x4 *>(prow + d) = v;
+                    if (d < D)
+                        *reinterpret_cast<f32x4 *>(prow + d) = v;
                 }
         }
         return;
@@ -729,7 +726,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
                 const int d = db * 32 + i4 * 8 + 4 * hi;
                 f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
                            o[db][4 * i4 + 3] * inv};
-                *reinterpret_cast<f32x4 *>(orow + d) = v;
+                if (d < D)
+                    *reinterpret_cast<f32x4 *>(orow + d) = v;
             }
     }
 }
@@ -1116,8 +1114,8 @@ static int device_cus() {
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
-                                  float *O, int Hq, int Hkv, int Sq, int Sk, float c, float *pm,
-                                  float *pl, float *pacc, long slots, hipStream_t st) {
+                                  float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
+                                  float *pm, float *pl, float *pacc, long slots, hipStream_t st) {
     constexpr int BQ = NW * 32;
     const int nqt = (Sq + BQ - 1) / BQ;
     long nblk = (long)Hq * nqt;
@@ -1134,12 +1132,12 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
-                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, c, nqt, split_first, pm,
+                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
                        pl, pacc, prows);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || split_first < 0)
         return e;
-    return launch_merge(pm, pl, pacc, O, (long)Hq * prows, DP, 2, c, prows, split_first * BQ, Sq,
+    return launch_merge(pm, pl, pacc, O, (long)Hq * prows, D, 2, c, prows, split_first * BQ, Sq,
                         st);
 }
 
@@ -1163,21 +1161,21 @@ static int prefill_waves(int Hq, int Sq, bool causal) {
 
 template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                                 int Hq, int Hkv, int Sq, int Sk, float c, float *pm, float *pl,
-                                 float *pacc, long slots, hipStream_t st) {
-    if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
-        if (prefill_waves(Hq, Sq, CAUSAL) == 8)
-            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c,
-                                                                 pm, pl, pacc, slots, st);
-    // 4-wave workgroups at D = 128 take 64-key tiles: at 128 keys the tiles use 128-136 KB of
-    // LDS and a CU could hold only one such workgroup (one wave per SIMD).
-    constexpr int KT4 = (DP == 128 && KT == 128) ? 64 : KT;
-    return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
-                                                          pacc, slots, st);
+                                 int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
+                                 float *pl, float *pacc, long slots, hipStream_t st) {
+    if (prefill_waves(Hq, Sq, CAUSAL) == 8)
+        return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
+                                                             pl, pacc, slots, st);
+    // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
+    // and a CU could hold only one such workgroup (one wave per SIMD).
+    constexpr int KT4 = (DP > 64 && KT == 128) ? 64 : KT;
+    return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
+                                                          pl, pacc, slots, st);
 }
 
-// The fast kernel needs D == DP, 16-byte vectors (vec; with V^T also Sk % 8 == 0, which the host
-// folds into vec) and a kv head's bytes within a buffer's 31-bit range.
+// The fast kernel needs D % 8 == 0 with D <= DP, 16-byte vectors (vec; with V^T also
+// Sk % 8 == 0, which the host folds into vec) and a kv head's bytes within a buffer's 31-bit
+// range. D in (64, 96] takes the 96-wide instance, whose MFMA tiles waste less on padding.
 // The general kernel keeps a 64-key tile at DP = 128: its 4-wave tiling at 128 keys would need
 // all 256 registers and drop to one wave per SIMD.
 template <int DP, int KT>
@@ -1186,13 +1184,18 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
                              float c, float *pm, float *pl, float *pacc, long slots,
                              hipStream_t st) {
     constexpr int KTG = (DP == 128 && KT == 128) ? 64 : KT;
-    const bool fast = vec && D == DP && (long)Sk * DP * 2 < 0x7fffffffL;
+    const bool fast = vec && D % 8 == 0 && D <= DP && (long)Sk * D * 2 < 0x7fffffffL;
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vt != 0, [&](auto VTF) {
             constexpr bool kC = decltype(CA)::value, kT = decltype(VTF)::value;
-            if (fast)
-                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, c, pm, pl,
-                                                             pacc, slots, st);
+            if (fast) {
+                if constexpr (DP == 128)
+                    if (D <= 96)
+                        return launch_prefill_fast_t<96, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
+                                                                     c, pm, pl, pacc, slots, st);
+                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
+                                                             pl, pacc, slots, st);
+            }
             return with_flag(vec != 0, [&](auto VE) {
                 return launch_prefill_t<DP, KTG, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
                                                                                Sq, Sk, D, c, st);
