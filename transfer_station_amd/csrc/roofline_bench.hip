@@ -254,13 +254,14 @@ __global__ __launch_bounds__(256) void valu_rate(float *out, int iters) {
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 template <bool TR>
-__global__ __launch_bounds__(256) void lds_rate(unsigned *out, int iters) {
+__global__ __launch_bounds__(256) void lds_rate(unsigned *out, unsigned long long *clk, int iters) {
     __shared__ __attribute__((aligned(16))) unsigned short tile[32768];
     for (int i = threadIdx.x; i < 32768; i += 256)
         tile[i] = (unsigned short)i;
     __syncthreads();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     unsigned acc = 0;
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -278,7 +279,12 @@ __global__ __launch_bounds__(256) void lds_rate(unsigned *out, int iters) {
             }
         }
     }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     out[blockIdx.x * blockDim.x + threadIdx.x] = acc;
+    if (threadIdx.x == 0) {
+        clk[2 * blockIdx.x] = t1 - t0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
 }
 
 // dst[i] = src[i] for i < n4 (float4 elements), grid-stride.
@@ -542,14 +548,17 @@ static double run_valu(bool exp) {
     return best;
 }
 
-// Bytes per clock per CU delivered by LDS reads.
-static double run_lds(bool tr) {
-    int cus = 0, clk_khz = 0;
+// Bytes per shader clock per CU delivered by LDS reads (clock from s_memtime over the 100 MHz
+// s_memrealtime inside the kernel), with wpc waves per CU.
+static double run_lds(bool tr, int wpc) {
+    int cus = 0;
     CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
-    CHECK(hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeClockRate, 0));
-    const int blocks = cus * 2, threads = 256, iters = 4000;
+    const int blocks = cus * wpc / 4, threads = 256, iters = 4000;
     unsigned *out;
+    unsigned long long *clk;
     CHECK(hipMalloc(&out, (size_t)blocks * threads * sizeof(unsigned)));
+    CHECK(hipMalloc(&clk, (size_t)blocks * 2 * sizeof(unsigned long long)));
+    std::vector<unsigned long long> hc((size_t)blocks * 2);
     hipEvent_t a, b;
     CHECK(hipEventCreate(&a));
     CHECK(hipEventCreate(&b));
@@ -557,18 +566,24 @@ static double run_lds(bool tr) {
     for (int rep = 0; rep < 3; ++rep) {
         CHECK(hipEventRecord(a, 0));
         if (tr)
-            hipLaunchKernelGGL(lds_rate<true>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+            hipLaunchKernelGGL(lds_rate<true>, dim3(blocks), dim3(threads), 0, 0, out, clk, iters);
         else
-            hipLaunchKernelGGL(lds_rate<false>, dim3(blocks), dim3(threads), 0, 0, out, iters);
+            hipLaunchKernelGGL(lds_rate<false>, dim3(blocks), dim3(threads), 0, 0, out, clk, iters);
         CHECK(hipGetLastError());
         CHECK(hipEventRecord(b, 0));
-        double ms = time_ms(a, b);
-        double bytes = (double)blocks * threads * iters * 8 * (tr ? 8 : 16);
-        double bpc = bytes / cus / (ms * 1e-3 * clk_khz * 1e3);
+        const double ms = time_ms(a, b);
+        CHECK(hipMemcpy(hc.data(), clk, hc.size() * sizeof(unsigned long long),
+                        hipMemcpyDeviceToHost));
+        double ghz = 0;
+        for (int i = 0; i < blocks; ++i)
+            ghz += (double)hc[2 * i] / (double)hc[2 * i + 1] * 0.1 / blocks;
+        const double bytes = (double)blocks * threads * iters * 8 * (tr ? 8 : 16);
+        const double bpc = bytes / cus / (ms * 1e-3 * ghz * 1e9);
         if (bpc > best)
             best = bpc;
     }
     CHECK(hipFree(out));
+    CHECK(hipFree(clk));
     return best;
 }
 
@@ -637,8 +652,10 @@ int main(int argc, char **argv) {
                    "\"chain4_tflops\": %.1f}\n",
                    w, run_chain(1, w), run_chain(2, w), run_chain(4, w));
     } else if (!strcmp(mode, "lds")) {
-        printf("{\"lds_read_b128_bytes_per_clk_cu\": %.1f, \"lds_read_tr_b64_bytes_per_clk_cu\": %.1f}\n",
-               run_lds(false), run_lds(true));
+        for (int wpc = 4; wpc <= 8; wpc += 4) // 64 KB of LDS per block: at most 2 per CU
+            printf("{\"waves_per_cu\": %d, \"lds_read_b128_bytes_per_clk_cu\": %.1f, "
+                   "\"lds_read_tr_b64_bytes_per_clk_cu\": %.1f}\n",
+                   wpc, run_lds(false, wpc), run_lds(true, wpc));
     } else if (!strcmp(mode, "valu")) {
         printf("{\"exp_chain_steps_per_simd_clk\": %.4f, \"fma_per_simd_clk\": %.4f}\n",
                run_valu(true), run_valu(false));
