@@ -1163,9 +1163,10 @@ template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
-    if (prefill_waves(Hq, Sq, CAUSAL) == 8)
-        return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
-                                                             pl, pacc, slots, st);
+    if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
+        if (prefill_waves(Hq, Sq, CAUSAL) == 8)
+            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
+                                                                 pm, pl, pacc, slots, st);
     // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
     // and a CU could hold only one such workgroup (one wave per SIMD).
     constexpr int KT4 = (DP > 64 && KT == 128) ? 64 : KT;
