@@ -356,8 +356,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill, fast path: D == DP (64 or 128) and 16-byte aligned tensors. The MFMA tiling of
-// attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per SIMD), plus:
+// Prefill, fast path: D % 8 == 0 with D <= DP (64, 96 or 128) and 16-byte aligned tensors; the
+// head-dim columns D .. DP-1 are zero in the tiles and in Q, and are never stored. The MFMA
+// tiling of attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per
+// SIMD; 4 on grids too small to fill the GPU), plus:
 //   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
 //     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
 //     offset (the range-checked one); the scalar offset is always 0. They are LDS-DMA loads
