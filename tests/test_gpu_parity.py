@@ -268,6 +268,8 @@ def test_bk_invariance(oracle):
     (2, 4096, 128, 0),  # 16-byte path, full tiles
     (2, 8, 8, 0),       # 16-byte path, one chunk per row
     (2, 64, 64, 2),     # misaligned by one element: element-wise path
+    (65535 + 7, 8, 8, 0),  # more kv heads than one launch's z range: two launches
+    (65535 + 2, 9, 7, 0),  # the same on the element-wise path
 ])
 def test_pack_v_full_transposes_exactly(Hkv, Sk, D, offset):
     rng = np.random.default_rng(Sk * 1000 + D)

@@ -1299,16 +1299,27 @@ extern "C" int attn_hip_launch_merge(const float *pm, const float *pl, const flo
 
 extern "C" int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D,
                                       void *stream) {
-    if (Hkv <= 0 || Sk <= 0 || D <= 0 || Hkv > 65535)
+    if (Hkv <= 0 || Sk <= 0 || D <= 0)
         return (int)hipErrorInvalidValue;
-    if (D % 8 == 0 && Sk % 8 == 0 && (((uintptr_t)V | (uintptr_t)Vp) & 15u) == 0) {
-        dim3 grid((unsigned)((Sk + 63) / 64), (unsigned)((D + 63) / 64), (unsigned)Hkv);
-        hipLaunchKernelGGL(attn_pack_v16_kernel, grid, dim3(256), 0, (hipStream_t)stream, V, Vp,
-                           Sk, D);
-        return (int)hipGetLastError();
+    const bool v16 = D % 8 == 0 && Sk % 8 == 0 && (((uintptr_t)V | (uintptr_t)Vp) & 15u) == 0;
+    // The kv head is the grid's z index, at most 65535 per launch: larger Hkv runs in chunks
+    // (each chunk's base stays 16-byte aligned, since Sk*D is a multiple of 8 on the v16 path).
+    constexpr int kMaxZ = 65535;
+    for (int h0 = 0; h0 < Hkv; h0 += kMaxZ) {
+        const unsigned nh = (unsigned)min(kMaxZ, Hkv - h0);
+        const size_t off = (size_t)h0 * Sk * D;
+        if (v16) {
+            dim3 grid((unsigned)((Sk + 63) / 64), (unsigned)((D + 63) / 64), nh);
+            hipLaunchKernelGGL(attn_pack_v16_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                               V + off, Vp + off, Sk, D);
+        } else {
+            dim3 grid((unsigned)((Sk + 31) / 32), (unsigned)((D + 31) / 32), nh);
+            hipLaunchKernelGGL(attn_pack_v_kernel, grid, dim3(32, 8), 0, (hipStream_t)stream,
+                               V + off, Vp + off, Sk, D);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return (int)e;
     }
-    dim3 grid((unsigned)((Sk + 31) / 32), (unsigned)((D + 31) / 32), (unsigned)Hkv);
-    hipLaunchKernelGGL(attn_pack_v_kernel, grid, dim3(32, 8), 0, (hipStream_t)stream, V, Vp, Sk,
-                       D);
-    return (int)hipGetLastError();
+    return (int)hipSuccess;
 }
