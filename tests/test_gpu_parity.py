@@ -453,3 +453,35 @@ def test_random_shapes(oracle, case):
         O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
     check(oracle, "random %d%s" % (i, " V^T" if vt else ""), Q, K, V, Hq, Hkv, Sq, Sk, D, causal,
           bk, ref_cap=8, O=O)
+
+
+# ---- a kv head past 2 GiB: K and V exceed a buffer's 31-bit range, so the prefill takes the
+# general kernel (64-bit element offsets), and decode and the V^T path read past 2 GiB as well --
+def _spread_bf16(n, seed):
+    """n finite bf16 values: random sign and mantissa, magnitude in [2^-7, 2), so that an offset
+    that wrapped at 2^31 bytes would read different values."""
+    x = np.random.default_rng(seed).integers(0, 1 << 16, size=n, dtype=np.uint16)
+    e = (np.uint16(120) + ((x >> np.uint16(7)) & np.uint16(7))) << np.uint16(7)
+    return (x & np.uint16(0x807F)) | e
+
+
+@pytest.fixture(scope="module")
+def kv_over_2gib():
+    """One kv head (D = 128) whose K is 2^31 + 18 KiB bytes, made once for the cases below."""
+    D = 128
+    Sk = (1 << 31) // (2 * D) + 72
+    say("generating K and V of %d keys x %d (2 x %.2f GB)" % (Sk, D, Sk * D * 2 / 1e9))
+    return Sk, D, _spread_bf16(Sk * D, 11), _spread_bf16(Sk * D, 12)
+
+
+@pytest.mark.parametrize("Hq,Sq,causal,prepack", [
+    (2, 40, 1, False),   # prefill, general kernel, causal
+    (2, 1, 0, False),    # split-K decode
+    (2, 40, 0, True),    # prefill from V^T packed on the device
+], ids=["prefill-causal", "decode", "prefill-vt"])
+def test_kv_head_over_2gib(oracle, kv_over_2gib, Hq, Sq, causal, prepack):
+    Sk, D, K, V = kv_over_2gib
+    Q = _spread_bf16(Hq * Sq * D, 13)
+    say("running Hq=%d Sq=%d causal=%d prepack_v=%d" % (Hq, Sq, causal, prepack))
+    O = ts.run_attention(Q, K, V, Hq, 1, Sq, Sk, D, causal, 128, prepack_v=prepack)
+    check(oracle, "kv head over 2 GiB", Q, K, V, Hq, 1, Sq, Sk, D, causal, 128, ref_cap=2, O=O)
