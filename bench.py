@@ -137,7 +137,7 @@ def measured_peaks():
     return out
 
 
-def cpu_baseline(o, ts, budget_s=12.0):
+def cpu_baseline(o, ts, budget_s=16.0):
     """The oracle on the headline workload's rows, 1 thread and all (<=16) threads."""
     B, Hq, Hkv, S, D = 4, 32, 8, 4096, 128
     Q, K, V = ts.synth_normal_qkv(B * Hq, B * Hkv, S, S, D, SEED0 + 3)
@@ -145,7 +145,8 @@ def cpu_baseline(o, ts, budget_s=12.0):
     out = {}
     nthreads = min(16, os.cpu_count() or 1)
     for label, nt in (("1", 1), ("all", nthreads)):
-        # grow the row sample until the run takes a meaningful time, within the budget
+        # grow the row sample (up to 64 rows of each of the B*Hq heads) until the run takes a
+        # meaningful time, within the budget
         ref_cap, heads, dt = 2, 1, 0.0
         while True:
             rows = o.ref_rowset(S, ref_cap)
@@ -154,12 +155,12 @@ def cpu_baseline(o, ts, budget_s=12.0):
                        V[: max(1, heads // 4) * S * D], heads, max(1, heads // 4), S, S, D, 0,
                        rows, nthreads=nt)
             dt = time.perf_counter() - t0
-            if dt > budget_s / 4 or ref_cap * heads >= 4096:
+            if dt > budget_s / 4 or (ref_cap >= 64 and heads >= B * Hq):
                 break
             if ref_cap < 64:
                 ref_cap *= 2
             else:
-                heads *= 2
+                heads = min(2 * heads, B * Hq)
         nrows = len(rows) * heads
         out[label] = {"rows": nrows, "seconds": dt, "tflops": nrows * flop_per_row / dt / 1e12,
                       "threads": nt}

@@ -121,6 +121,12 @@ def attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, rows=None, nthreads=1, out=Non
         rows = np.arange(Sq, dtype=np.int32)
     rows = np.ascontiguousarray(rows, dtype=np.int32)
     O = out if out is not None else np.zeros(Hq * Sq * D, np.float32)
+    # the C oracle indexes raw pointers: the arrays must hold the shapes they are said to have
+    if (np.asarray(Q).size < Hq * Sq * D or np.asarray(K).size < Hkv * Sk * D or
+            np.asarray(V).size < Hkv * Sk * D or O.size < Hq * Sq * D):
+        raise ValueError("attn_ref: an array is smaller than its (H, S, D) shape")
+    if rows.size and (rows.min() < 0 or rows.max() >= Sq):
+        raise ValueError("attn_ref: a row index is outside [0, Sq)")
     if nthreads == 1:
         rc = lib().orc_attn_ref(Q, K, V, O, Hq, Hkv, Sq, Sk, D, int(causal), rows, rows.size)
     else:

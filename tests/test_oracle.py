@@ -245,3 +245,18 @@ def test_oracle_vs_torch_sdpa_float64(oracle, case):
             q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), attn_mask=allowed,
             scale=float(1.0 / np.sqrt(np.float32(D)))).squeeze(0).numpy()
         assert np.abs(R - sd).max() / np.abs(sd).max() < 1e-5
+
+
+def test_attn_ref_rejects_short_arrays(oracle):
+    """The C oracle indexes raw pointers, so its wrapper refuses arrays smaller than the shape
+    they are passed with, and rows outside [0, Sq)."""
+    Hq, Hkv, Sq, Sk, D = 4, 2, 5, 7, 8
+    Q = np.zeros(Hq * Sq * D, np.uint16)
+    K = np.zeros(Hkv * Sk * D, np.uint16)
+    V = np.zeros(Hkv * Sk * D, np.uint16)
+    oracle.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, 0)
+    for args in ((Q[:-1], K, V), (Q, K[:-1], V), (Q, K, V[:-1])):
+        with pytest.raises(ValueError):
+            oracle.attn_ref(*args, Hq, Hkv, Sq, Sk, D, 0)
+    with pytest.raises(ValueError):
+        oracle.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, rows=np.array([0, Sq], np.int32))
