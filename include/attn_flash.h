@@ -41,7 +41,7 @@ extern "C" {
 #define ATTN_SCRATCH_ALIGN 64
 
 /* Largest head dimension the compiled kernels accept (the reference has no bound). */
-#define ATTN_D_MAX 128
+#define ATTN_D_MAX 256
 
 /* Optional per-call timing (flash.c:704-706). The GPU kernel is one fused launch, so the
  * whole kernel time (HIP events, seconds) is ADDED to qxk; packv, softmax and sxv are

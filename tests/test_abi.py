@@ -117,7 +117,7 @@ def test_bad_bk_aborts_at_both_doors(bk):
     ("1, 2, 3, 4, 4, 4, 0, 8, 64, 0, 128, 64", "Sq >= 1"),
     ("1, 2, 3, 4, 4, 4, 8, 0, 64, 0, 128, 64", "Sk >= 1"),
     ("1, 2, 3, 4, 4, 4, 8, 8, 0, 0, 128, 64", "D=0 is invalid"),
-    ("1, 2, 3, 4, 4, 4, 8, 8, 129, 0, 128, 64", "D=129 is invalid"),
+    ("1, 2, 3, 4, 4, 4, 8, 8, 257, 0, 128, 64", "D=257 is invalid"),
     ("1, 2, 3, 4, 4, 4, 8, 8, 64, 0, 128, 0", "scratch must be"),
     ("1, 2, 3, 4, 4, 4, 8, 8, 64, 0, 128, 65", "scratch must be"),
     ("0, 2, 3, 4, 4, 4, 8, 8, 64, 0, 128, 64", "device pointers"),

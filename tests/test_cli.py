@@ -41,7 +41,7 @@ def run(cli, *args, timeout=300):
     (["--shape", "3,2,8,8,64"], "bad --shape"),
     (["--shape", "4,4,0,8,64"], "bad --shape"),
     (["--shape", "4,4"], "bad --shape: need Hq,Hkv,Sq,Sk,D"),
-    (["--shape", "4,4,8,8,256"], "exceeds ATTN_D_MAX"),
+    (["--shape", "4,4,8,8,257"], "exceeds ATTN_D_MAX"),
     (["--frobnicate"], "unknown argument: --frobnicate"),
     (["--no-softmax"], "--no-softmax: not available"),
 ])

@@ -183,11 +183,33 @@ def test_tail_probe(oracle, bk, causal, D):
             check(oracle, "tail", Q, K, V, 4, 2, Sq, Sk, D, causal, bk)
 
 
-@pytest.mark.parametrize("D", [1, 2, 3, 7, 8, 16, 24, 33, 40, 63, 64, 65, 72, 100, 127, 128])
+@pytest.mark.parametrize("D", [1, 2, 3, 7, 8, 16, 24, 33, 40, 63, 64, 65, 72, 100, 127, 128, 129,
+                               160, 200, 255, 256])
 def test_head_dim_sweep(oracle, D):
     for Sq, Hq, Hkv in ((37, 4, 2), (1, 8, 2)):
         Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, 150, D, 1000 + D)
         check(oracle, "D sweep", Q, K, V, Hq, Hkv, Sq, 150, D, 1, 64)
+
+
+# ---- head dims past 128 (up to ATTN_D_MAX = 256): the general prefill kernel on 32-key tiles
+# and the 256-wide decode kernel ----------------------------------------------------------------
+@pytest.mark.parametrize("shape", [
+    (8, 2, 300, 700, 256, 1, 64, 0),     # GQA prefill, causal, bk 64
+    (16, 4, 200, 333, 256, 0, 4096, 0),  # prefill, Sk % 8 != 0, one scratch for the largest bk
+    (32, 8, 1, 4096, 256, 0, 128, 0),    # split-K decode
+    (8, 1, 5, 1001, 192, 1, 128, 0),     # decode row blocks, D = 192
+    (8, 2, 300, 640, 256, 1, 128, 1),    # prefill from V^T
+    (8, 2, 1, 2048, 256, 0, 128, 1),     # decode from V^T
+], ids=["prefill-causal", "prefill-ragged", "decode", "decode-d192", "prefill-vt", "decode-vt"])
+def test_head_dim_256(oracle, shape):
+    Hq, Hkv, Sq, Sk, D, causal, bk, vt = shape
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 256 + Sk)
+    if vt:
+        vt_host = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
+        O = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=1)
+    else:
+        O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk)
+    check(oracle, "D=%d" % D, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, ref_cap=8, O=O)
 
 
 def test_sk_one_copies_v(oracle):

@@ -16,7 +16,7 @@ ATTN_BK_MIN = 16
 ATTN_BK_MAX = 4096
 ATTN_BK_DEFAULT = 128
 ATTN_SCRATCH_ALIGN = 64
-ATTN_D_MAX = 128
+ATTN_D_MAX = 256
 
 
 class AttnTimes(ctypes.Structure):

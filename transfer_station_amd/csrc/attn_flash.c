@@ -161,7 +161,7 @@ static void attn_decode_split(int Hq, int Hkv, int Sq, int Sk, int nrb, int *nsp
     *kps_o = (int)kps;
 }
 
-static int attn_dp_for_d(int D) { return (D <= 64) ? 64 : 128; }
+static int attn_dp_for_d(int D) { return (D <= 64) ? 64 : (D <= 128 ? 128 : 256); }
 
 /* ---- timing events (only when the caller asks for tm) ------------------------------------- */
 static _Thread_local hipEvent_t t_ev0 = NULL, t_ev1 = NULL;

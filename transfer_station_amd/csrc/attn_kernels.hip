@@ -14,7 +14,7 @@
 // Kernels:
 //   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D % 8 == 0, D <= DP in
 //                                          {64, 96, 128}; one workgroup = NW waves x 32 rows
-//   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 128 and alignment
+//   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
 //   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
@@ -1187,17 +1187,19 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
                              float c, float *pm, float *pl, float *pacc, long slots,
                              hipStream_t st) {
     constexpr int KTG = (DP == 128 && KT == 128) ? 64 : KT;
-    const bool fast = vec && D % 8 == 0 && D <= DP && (long)Sk * D * 2 < 0x7fffffffL;
+    const bool fast = DP <= 128 && vec && D % 8 == 0 && D <= DP && (long)Sk * D * 2 < 0x7fffffffL;
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vt != 0, [&](auto VTF) {
             constexpr bool kC = decltype(CA)::value, kT = decltype(VTF)::value;
-            if (fast) {
-                if constexpr (DP == 128)
-                    if (D <= 96)
-                        return launch_prefill_fast_t<96, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
-                                                                     c, pm, pl, pacc, slots, st);
-                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
-                                                             pl, pacc, slots, st);
+            if constexpr (DP <= 128) {
+                if (fast) {
+                    if constexpr (DP == 128)
+                        if (D <= 96)
+                            return launch_prefill_fast_t<96, KT, kC, kT>(
+                                Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm, pl, pacc, slots, st);
+                    return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
+                                                                 c, pm, pl, pacc, slots, st);
+                }
             }
             return with_flag(vec != 0, [&](auto VE) {
                 return launch_prefill_t<DP, KTG, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
@@ -1212,18 +1214,27 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
                             int kt, float c, float *pm, float *pl, float *pacc, long slots,
                             hipStream_t st) {
-    switch (kt) {
-    case 32:
-        return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
-                                         pl, pacc, slots, st);
-    case 64:
-        return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
-                                         pl, pacc, slots, st);
-    case 128:
-        return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
+    // D in (128, 256]: the general kernel on 32-key tiles (its staging registers and the
+    // 256-wide O accumulator leave no room for larger tiles); bk keeps its meaning as the
+    // online-softmax granularity upper bound, as for the 64-key cap at D = 128.
+    if constexpr (DP == 256) {
+        (void)kt;
+        return launch_prefill_dk<256, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
                                           pl, pacc, slots, st);
-    default:
-        return hipErrorInvalidValue;
+    } else {
+        switch (kt) {
+        case 32:
+            return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
+                                             pm, pl, pacc, slots, st);
+        case 64:
+            return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
+                                             pm, pl, pacc, slots, st);
+        case 128:
+            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
+                                              pm, pl, pacc, slots, st);
+        default:
+            return hipErrorInvalidValue;
+        }
     }
 }
 
@@ -1267,6 +1278,9 @@ extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, con
     case 128:
         return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
                                           pm, pl, pacc, slots, st);
+    case 256:
+        return (int)launch_prefill_d<256>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+                                          pm, pl, pacc, slots, st);
     default:
         return (int)hipErrorInvalidValue;
     }
@@ -1285,6 +1299,9 @@ extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, cons
                                         vt, c, nsplit, kps, nrb, st);
     case 128:
         return (int)launch_decode_d<128>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal,
+                                         vec, vt, c, nsplit, kps, nrb, st);
+    case 256:
+        return (int)launch_decode_d<256>(Q, K, V, O, pm, pl, pacc, Hq, Hkv, Sq, Sk, D, causal,
                                          vec, vt, c, nsplit, kps, nrb, st);
     default:
         return (int)hipErrorInvalidValue;
