@@ -200,7 +200,10 @@ def test_head_dim_sweep(oracle, D):
     (8, 1, 5, 1001, 192, 1, 128, 0),     # decode row blocks, D = 192
     (8, 2, 300, 640, 256, 1, 128, 1),    # prefill from V^T
     (8, 2, 1, 2048, 256, 0, 128, 1),     # decode from V^T
-], ids=["prefill-causal", "prefill-ragged", "decode", "decode-d192", "prefill-vt", "decode-vt"])
+    (8, 2, 200, 500, 224, 1, 16, 0),     # 32-key tiles, causal key split, D = 224
+    (6, 3, 130, 70, 200, 1, 128, 0),     # general kernel (D % 8 != 0)
+], ids=["prefill-causal", "prefill-ragged", "decode", "decode-d192", "prefill-vt", "decode-vt",
+        "kt32-split-d224", "general-d200"])
 def test_head_dim_256(oracle, shape):
     Hq, Hkv, Sq, Sk, D, causal, bk, vt = shape
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 256 + Sk)

@@ -13,7 +13,7 @@
 //
 // Kernels:
 //   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D % 8 == 0, D <= DP in
-//                                          {64, 96, 128}; one workgroup = NW waves x 32 rows
+//                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
@@ -356,10 +356,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill, fast path: D % 8 == 0 with D <= DP (64, 96 or 128) and 16-byte aligned tensors; the
-// head-dim columns D .. DP-1 are zero in the tiles and in Q, and are never stored. The MFMA
-// tiling of attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two waves per
-// SIMD; 4 on grids too small to fill the GPU), plus:
+// Prefill, fast path: D % 8 == 0 with D <= DP (64, 96, 128 or 256) and 16-byte aligned
+// tensors; the head-dim columns D .. DP-1 are zero in the tiles and in Q, and are never stored.
+// The MFMA tiling of attn_prefill_kernel with NW waves per workgroup (8: 256 query rows, two
+// waves per SIMD; 4 on grids too small to fill the GPU, and always at DP = 256, where one wave
+// per SIMD holds O and Q), plus:
 //   * K/V tiles arrive through raw buffer loads whose range is the kv head's Sk*D*2 bytes, so a
 //     key past Sk reads as zero without a branch. The whole byte offset travels in the VGPR
 //     offset (the range-checked one); the scalar offset is always 0. They are LDS-DMA loads
@@ -397,7 +398,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, u
 }
 
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
+__global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
@@ -498,7 +499,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void attn_prefill_fast_kernel(
     // A chunk of columns D and beyond gets an offset past the buffer's range and arrives as zero.
     constexpr int NI = KT * DP / 512;
     constexpr int PW = (NI + NW - 1) / NW;
-    static_assert(PW >= 1 && PW <= 4, "DMA blocks per wave");
+    static_assert(PW >= 1 && PW <= 8, "DMA blocks per wave");
     const int nblk_w = max(0, min(PW, NI - w * PW)); // this wave's blocks (wave-uniform)
     uint32_t kso[PW], vso[PW];
 #pragma unroll
@@ -1165,12 +1166,13 @@ template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
-    if constexpr (KT * DP / 8 >= 512) // every thread of 8 waves stages at least one chunk
+    if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (prefill_waves(Hq, Sq, CAUSAL) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
                                                                  pm, pl, pacc, slots, st);
     // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
-    // and a CU could hold only one such workgroup (one wave per SIMD).
+    // and a CU could hold only one such workgroup (one wave per SIMD). At D > 128 the O and Q
+    // registers allow only one wave per SIMD anyway, so that is the only shape there.
     constexpr int KT4 = (DP > 64 && KT == 128) ? 64 : KT;
     return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
                                                           pl, pacc, slots, st);
@@ -1186,20 +1188,18 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
                              int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
                              float c, float *pm, float *pl, float *pacc, long slots,
                              hipStream_t st) {
-    constexpr int KTG = (DP == 128 && KT == 128) ? 64 : KT;
-    const bool fast = DP <= 128 && vec && D % 8 == 0 && D <= DP && (long)Sk * D * 2 < 0x7fffffffL;
+    constexpr int KTG = (DP == 256) ? 32 : ((DP == 128 && KT == 128) ? 64 : KT);
+    const bool fast = vec && D % 8 == 0 && D <= DP && (long)Sk * D * 2 < 0x7fffffffL;
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vt != 0, [&](auto VTF) {
             constexpr bool kC = decltype(CA)::value, kT = decltype(VTF)::value;
-            if constexpr (DP <= 128) {
-                if (fast) {
-                    if constexpr (DP == 128)
-                        if (D <= 96)
-                            return launch_prefill_fast_t<96, KT, kC, kT>(
-                                Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm, pl, pacc, slots, st);
-                    return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
-                                                                 c, pm, pl, pacc, slots, st);
-                }
+            if (fast) {
+                if constexpr (DP == 128)
+                    if (D <= 96)
+                        return launch_prefill_fast_t<96, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
+                                                                     c, pm, pl, pacc, slots, st);
+                return launch_prefill_fast_t<DP, KT, kC, kT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
+                                                             pl, pacc, slots, st);
             }
             return with_flag(vec != 0, [&](auto VE) {
                 return launch_prefill_t<DP, KTG, kC, decltype(VE)::value, kT>(Q, K, V, O, Hq, Hkv,
@@ -1214,12 +1214,14 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
                             int kt, float c, float *pm, float *pl, float *pacc, long slots,
                             hipStream_t st) {
-    // D in (128, 256]: the general kernel on 32-key tiles (its staging registers and the
-    // 256-wide O accumulator leave no room for larger tiles); bk keeps its meaning as the
-    // online-softmax granularity upper bound, as for the 64-key cap at D = 128.
+    // D in (128, 256]: key tiles of at most 64 keys (the fast kernel's two 64-key K and V
+    // tiles fill 128 KB of LDS); the general kernel there always takes 32-key tiles, since its
+    // staging registers and the 256-wide O accumulator leave no room for more.
     if constexpr (DP == 256) {
-        (void)kt;
-        return launch_prefill_dk<256, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
+        if (kt <= 32)
+            return launch_prefill_dk<256, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
+                                              pm, pl, pacc, slots, st);
+        return launch_prefill_dk<256, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
                                           pl, pacc, slots, st);
     } else {
         switch (kt) {
