@@ -215,6 +215,30 @@ def test_head_dim_256(oracle, shape):
     check(oracle, "D=%d" % D, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, ref_cap=8, O=O)
 
 
+# ---- short query blocks under GQA (Sq below a workgroup's rows, g*Sq > 64): the g heads' rows
+# of a kv head are packed into shared query tiles --------------------------------------------------
+@pytest.mark.parametrize("shape", [
+    (32, 8, 17, 1000, 128, 1, 0),   # 68 rows per kv head, causal
+    (32, 8, 40, 333, 128, 0, 0),    # 160 rows, Sk % 8 != 0
+    (64, 4, 5, 700, 64, 1, 0),      # g = 16, 80 rows
+    (16, 2, 100, 100, 96, 1, 0),    # Sq == Sk causal, D = 96
+    (8, 1, 200, 4096, 128, 1, 0),   # MQA, 1600 rows in 8-wave tiles
+    (32, 8, 33, 640, 128, 1, 1),    # V^T input
+    (24, 6, 50, 500, 256, 1, 0),    # D = 256
+], ids=["g4-sq17", "g4-sq40", "g16-sq5", "g8-sq100-d96", "mqa-sq200", "vt", "d256"])
+def test_gqa_packed_short_queries(oracle, shape):
+    Hq, Hkv, Sq, Sk, D, causal, vt = shape
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 700 + Sq)
+    if vt:
+        vt_host = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
+        O = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, 128, v_prepacked=1)
+    else:
+        O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
+    check(oracle, "packed", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128, O=O)
+    if causal and Sq > Sk:
+        assert np.all(O.reshape(Hq, Sq, D)[:, :Sq - Sk] == 0.0)
+
+
 def test_sk_one_copies_v(oracle):
     """Sk = 1: a one-element softmax. The kernels evaluate p = 2^(s*c - m*c) with one fma, so
     p at the row max is 1 within 2^-23 (not exactly 1, unlike the reference's exp(s - m)):

@@ -402,7 +402,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows) {
+    float *__restrict__ pacc, int prows, int pack) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -416,8 +416,15 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
     // is split in two (causal grids too small to fill the GPU), the half `part` (-1: whole).
     // Causal work grows with the query tile, so the items of a kv head are dispatched heaviest
     // first: longest-first keeps the tail of the grid short.
+    // pack (Sq below the workgroup's BQ rows, GQA groups): the g*Sq rows of a kv head are one
+    // row space, row r being query r % Sq of head u*g + r / Sq, and qt tiles it in BQ rows, so
+    // short query blocks fill whole tiles and a kv head's K/V is read once for all its heads.
     int h, qt, part = -1;
-    if (split_first < 0) {
+    if (pack) {
+        const int uu = L / nqt;
+        qt = L - uu * nqt;
+        h = uu * g;
+    } else if (split_first < 0) {
         const int uu = L / (g * nqt);
         const int rr = L - uu * (g * nqt);
         qt = CAUSAL ? nqt - 1 - rr / g : rr / g;
@@ -449,30 +456,53 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
     const int l32 = lane & 31, hi = lane >> 5;
-    const int q0 = qt * BQ + w * 32;
-    const int myq = q0 + l32;
+    // This lane's row: query myq of head hl (valid if rvalid); the wave's valid rows have query
+    // indices in [qmin, qmax] (causal limits), and the workgroup's at most qwg.
+    int hl, myq, qmin, qmax, qwg;
+    bool rvalid, wvalid;
+    if (pack) {
+        const int R = g * Sq;
+        const int r = qt * BQ + w * 32 + l32;
+        rvalid = r < R;
+        hl = h + (rvalid ? r / Sq : 0);
+        myq = rvalid ? r - (r / Sq) * Sq : 0;
+        const int r0 = qt * BQ + w * 32, r1 = min(r0 + 31, R - 1);
+        wvalid = r0 < R;
+        const bool one = r0 / Sq == r1 / Sq;
+        qmin = one ? r0 - (r0 / Sq) * Sq : 0;
+        qmax = one ? r1 - (r1 / Sq) * Sq : Sq - 1;
+        const int g0 = qt * BQ, g1 = min(g0 + BQ - 1, R - 1);
+        qwg = (g0 / Sq == g1 / Sq) ? g1 - (g1 / Sq) * Sq : Sq - 1;
+    } else {
+        hl = h;
+        myq = qt * BQ + w * 32 + l32;
+        rvalid = myq < Sq;
+        qmin = qt * BQ + w * 32;
+        wvalid = qmin < Sq;
+        qmax = min(qmin + 31, Sq - 1);
+        qwg = min(qt * BQ + BQ - 1, Sq - 1);
+    }
+    const size_t qrow = (size_t)hl * Sq + myq; // row of Q and O
 
-    const uint16_t *Qh = Q + (size_t)h * Sq * D;
     const uint32_t kvbytes = (uint32_t)Sk * D * 2;
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(V + (size_t)u * Sk * D, kvbytes); // V^T path
 
     bf16x8 qb[DP / 16];
 #pragma unroll
     for (int kk = 0; kk < DP / 16; ++kk)
-        qb[kk] = as_bf16x8(load_row8<true>(Qh, (size_t)myq, kk * 16 + hi * 8, D, myq < Sq));
+        qb[kk] = as_bf16x8(load_row8<true>(Q, qrow, kk * 16 + hi * 8, D, rvalid));
     // Q must be resident before the loop: otherwise the compiler's wait at the loop's first
     // MFMA also waits for the next tile's prefetch (its count cannot tell the two apart).
     // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
     __builtin_amdgcn_s_waitcnt(0x0F70);
 
     int nkt = (Sk + KT - 1) / KT;
-    int wave_maxkey = (q0 < Sq) ? Sk - 1 : -1;
+    int wave_maxkey = wvalid ? Sk - 1 : -1;
     if (CAUSAL) {
-        const int last_row = min(qt * BQ + BQ - 1, Sq - 1);
-        const int maxkey = Sk - Sq + last_row;
+        const int maxkey = Sk - Sq + qwg;
         nkt = (maxkey < 0) ? 0 : min(nkt, maxkey / KT + 1);
-        if (q0 < Sq)
-            wave_maxkey = min(Sk - 1, Sk - Sq + min(q0 + 31, Sq - 1));
+        if (wvalid)
+            wave_maxkey = min(Sk - 1, Sk - Sq + qmax);
     }
     const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + myq) : Sk - 1;
     const float lazy_raw = kLazyLog2 / c; // headroom in raw-score units
@@ -613,7 +643,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 }
             }
-            if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + q0)) {
+            if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin)) {
 #pragma unroll
                 for (int t = 0; t < KT / 32; ++t)
 #pragma unroll
@@ -700,7 +730,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
     if (part >= 0) {
         // Unnormalised partial of one key half: (m, l, acc) into slot (row, part) for the
         // log-sum-exp merge (attn_merge_kernel).
-        if (myq < Sq) {
+        if (rvalid) {
             const size_t slot = ((size_t)h * prows + (myq - split_first * BQ)) * 2 + part;
             if (hi == 0) {
                 pm[slot] = m_run;
@@ -720,8 +750,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
         return;
     }
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
-    if (myq < Sq) {
-        float *orow = O + ((size_t)h * Sq + myq) * D;
+    if (rvalid) {
+        float *orow = O + qrow * D;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
@@ -1112,6 +1142,13 @@ static int device_cus() {
     return cus[dev];
 }
 
+// Short query blocks under GQA (Sq <= 64, g > 1): the g heads' rows of a kv head share query
+// tiles instead of each head leaving all but one or two waves of its tile idle. Measured with
+// 64 batches x 32 heads (8 kv heads), Sk = 4096, causal, against one tile per head: Sq = 24 /
+// 32 / 48 / 64: 2.35x / 2.1x / 1.67x / 1.25x faster. From Sq ~ 100 up, one tile per head is
+// faster, since its larger grid keeps every CU busy.
+static bool prefill_pack(int Hq, int Hkv, int Sq) { return Hq / Hkv > 1 && Sq <= 64; }
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -1120,10 +1157,12 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                   float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
                                   float *pm, float *pl, float *pacc, long slots, hipStream_t st) {
     constexpr int BQ = NW * 32;
-    const int nqt = (Sq + BQ - 1) / BQ;
-    long nblk = (long)Hq * nqt;
+    const int g = Hq / Hkv;
+    const int pack = prefill_pack(Hq, Hkv, Sq) ? 1 : 0;
+    const int nqt = pack ? (g * Sq + BQ - 1) / BQ : (Sq + BQ - 1) / BQ;
+    long nblk = (long)(pack ? Hkv : Hq) * nqt;
     int split_first = -1, prows = 0;
-    if (CAUSAL && pm && nqt >= 2 && nblk <= device_cus()) {
+    if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus()) {
         const int sf = nqt / 2;
         const long pr = (long)Sq - (long)sf * BQ;
         if (pr > 0 && 2L * Hq * pr <= slots) {
@@ -1136,7 +1175,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
         return hipErrorInvalidValue;
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows);
+                       pl, pacc, prows, pack);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || split_first < 0)
         return e;
@@ -1145,12 +1184,17 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 }
 
 // Waves per workgroup for the fast prefill kernel: 8 (256 query rows, one workgroup per CU,
-// two waves per SIMD), or 4 (128 rows; two workgroups fit a CU) when 256-row tiles would leave
-// CUs idle: at most half as many 8-wave workgroups as CUs, or for causal grids (uneven tiles)
-// at most one per CU. Measured against 8 waves: 16 heads at 2k +21%, Qwen3 causal 1k / 2k / 4k
-// +18% / +9% / +7.5%, config 5 causal +24%; above those sizes 8 waves win by 5-9%.
+// two waves per SIMD), or 4 (128 rows; two workgroups fit a CU).
+//  * Packed tiles (prefill_pack): 4 waves when a kv head's rows fit one 128-row tile or fill
+//    128-row tiles better than 256-row ones.
+//  * Otherwise 4 waves when 256-row tiles are nearly full (>= 90% of their rows are queries)
+//    but would leave CUs idle: at most half as many 8-wave workgroups as CUs, or for causal
+//    grids (uneven tiles) at most one per CU. Measured against 8 waves: 16 heads at 2k +21%,
+//    Qwen3 causal 1k / 2k / 4k +18% / +9% / +7.5%, config 5 causal +24%. When 256-row tiles
+//    are part empty (Sq = 128, 200), 4 waves add no parallelism and their 64-key tiles lose
+//    11-20%; above the small-grid sizes 8 waves win by 5-9%.
 // ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
-static int prefill_waves(int Hq, int Sq, bool causal) {
+static int prefill_waves(int Hq, int Hkv, int Sq, bool causal) {
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
@@ -1158,8 +1202,16 @@ static int prefill_waves(int Hq, int Sq, bool causal) {
     }
     if (forced)
         return forced;
-    const long n8 = (long)Hq * ((Sq + 255) / 256);
-    return (n8 <= (causal ? device_cus() : device_cus() / 2)) ? 4 : 8;
+    const int g = Hq / Hkv;
+    if (prefill_pack(Hq, Hkv, Sq)) {
+        const long R = (long)g * Sq; // rows per kv head
+        const long t4 = (R + 127) / 128, t8 = (R + 255) / 256;
+        return (R <= 128 || 4 * t4 < 8 * t8) ? 4 : 8; // fewer idle wave slots at 4 waves
+    }
+    const long t8 = (Sq + 255) / 256;
+    const long n8 = (long)Hq * t8;
+    const bool full = (long)Sq * 10 >= t8 * 256 * 9;
+    return (full && n8 <= (causal ? device_cus() : device_cus() / 2)) ? 4 : 8;
 }
 
 template <int DP, int KT, bool CAUSAL, bool VT>
@@ -1167,7 +1219,7 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
-        if (prefill_waves(Hq, Sq, CAUSAL) == 8)
+        if (prefill_waves(Hq, Hkv, Sq, CAUSAL) == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
                                                                  pm, pl, pacc, slots, st);
     // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
