@@ -118,9 +118,23 @@ def test_decode_split_paths(oracle, Hkv, Sk):
     (4, 4, 17, 64, 64, 0),      # g = 1, Sq = 17
 ])
 def test_decode_row_blocks(oracle, Hq, Hkv, Sq, Sk, D, causal):
-    """Up to 64 query rows per kv head (g*Sq) take the split-K decode kernel in 16-row blocks."""
+    """Up to 64 query rows per kv head (g*Sq) take the split-K decode kernel in 16-row blocks
+    while there are fewer kv heads than CUs."""
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 60 + Sq)
     check(oracle, "decode row blocks", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
+
+
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
+    (1024, 256, 8, 300, 64, 1),   # 32 rows per kv head, 256 kv heads: packed prefill
+    (2048, 512, 16, 520, 128, 0), # 64 rows, 512 kv heads
+    (1024, 256, 4, 777, 128, 1),  # 16 rows: decode at any kv-head count
+])
+def test_short_queries_many_kv_heads(oracle, Hq, Hkv, Sq, Sk, D, causal):
+    """Decode-sized query blocks (g*Sq <= 64) over at least as many kv heads as CUs go to the
+    packed prefill tiles (up to 16 rows, to decode); the answer is the same either way."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 90 + Sq)
+    check(oracle, "short queries, many kv heads", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128,
+          ref_cap=4)
 
 
 @pytest.mark.parametrize("S", [1024, 2048, 4096])
@@ -373,7 +387,8 @@ def test_v_prepacked(oracle, case):
     vt_host = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
     direct = ts.run_attention(Q, K, vt_host, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=1)
     assert np.array_equal(packed.view(np.uint32), direct.view(np.uint32))
-    decode = (Hq // Hkv) * Sq <= 64
+    rows = (Hq // Hkv) * Sq
+    decode = rows <= 16 or (rows <= 64 and Hkv < 256)  # the host's choice on 256 CUs
     same_kernel = decode or D % 8 != 0 or Sk % 8 == 0
     if same_kernel:
         nd = int(np.count_nonzero(packed.view(np.uint32) != base.view(np.uint32)))

@@ -27,6 +27,7 @@ int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t 
 int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, float *O, int rows,
                           int D, int nsplit, float c, int Sq, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
+int attn_hip_device_cus(void);
 
 /* ---- device scratch layout ---------------------------------------------------------------
  * Split-K partial slots, one per (query row, split): m[ATTN_SLOTS], l[ATTN_SLOTS] and
@@ -136,7 +137,20 @@ static int attn_kt_for_bk(int bk, int dp) {
 }
 
 #define ATTN_DECODE_ROWS 16     /* query rows the decode MFMA tile holds (one row block) */
-#define ATTN_DECODE_MAX_ROWS 64 /* g*Sq rows per kv head up to which decode beats prefill */
+#define ATTN_DECODE_MAX_ROWS 64 /* g*Sq rows per kv head up to which decode can beat prefill */
+
+/* Decode (split-K over the key range, 16-row blocks) or prefill for g*Sq rows per kv head.
+ * Up to one row block decode streams K/V at the HBM rate. Up to 64 rows it wins while the
+ * prefill grid (one packed query tile per kv head) would be smaller than the GPU, since
+ * split-K spreads few kv heads over many workgroups; with at least as many kv heads as CUs
+ * the prefill's MFMA tiles win. Measured, Sk = 4096, 32-64 rows per kv head: 512 kv heads
+ * prefill 1.4-2.1x faster; 32-64 kv heads decode 1.7-2x faster. */
+static int attn_use_decode(int Hkv, int group, int Sq) {
+    const long rows = (long)group * Sq;
+    if (rows <= ATTN_DECODE_ROWS)
+        return 1;
+    return rows <= ATTN_DECODE_MAX_ROWS && Hkv < attn_hip_device_cus();
+}
 #define ATTN_DECODE_TARGET_WG 512
 #define ATTN_DECODE_MIN_KEYS 128 /* keys per split: one 32-key tile per wave, 4 waves */
 
@@ -203,7 +217,7 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         attn_events();
         attn_hip_check(hipEventRecord(t_ev0, (hipStream_t)st), who);
     }
-    if ((long)group * Sq <= ATTN_DECODE_MAX_ROWS) {
+    if (attn_use_decode(Hkv, group, Sq)) {
         const int nrb = (group * Sq + ATTN_DECODE_ROWS - 1) / ATTN_DECODE_ROWS;
         int nsplit, kps;
         attn_decode_split(Hq, Hkv, Sq, Sk, nrb, &nsplit, &kps);

@@ -1362,6 +1362,9 @@ extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, cons
     }
 }
 
+// Compute units of the current device, for the host layer's kernel choice.
+extern "C" int attn_hip_device_cus(void) { return device_cus(); }
+
 extern "C" int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc,
                                      float *O, int rows, int D, int nsplit, float c, int Sq,
                                      void *stream) {
