@@ -549,3 +549,36 @@ def test_kv_head_over_2gib(oracle, kv_over_2gib, Hq, Sq, causal, prepack):
     say("running Hq=%d Sq=%d causal=%d prepack_v=%d" % (Hq, Sq, causal, prepack))
     O = ts.run_attention(Q, K, V, Hq, 1, Sq, Sk, D, causal, 128, prepack_v=prepack)
     check(oracle, "kv head over 2 GiB", Q, K, V, Hq, 1, Sq, Sk, D, causal, 128, ref_cap=2, O=O)
+
+
+def _random_cases_wide(n, seed):
+    """Head dims past 128 (odd ones on the general kernel), short query blocks that pack the
+    GQA heads' rows, and many kv heads (the decode / packed-prefill choice)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice([136, 160, 192, 200, 224, 256, 130, 250, 64, 128]))
+        if rng.random() < 0.3:
+            Hkv, g = int(rng.integers(256, 300)), int(rng.choice([2, 4, 8]))
+            Sq = int(rng.integers(1, 17))
+            Sk = int(rng.integers(1, 200))
+        else:
+            Hkv, g = int(rng.integers(1, 4)), int(rng.choice([1, 2, 4, 8, 16]))
+            Sq = int(rng.integers(1, 65)) if rng.random() < 0.6 else int(rng.integers(65, 300))
+            Sk = int(rng.integers(1, 900))
+        causal = int(rng.random() < 0.5)
+        bk = int(rng.choice([16, 32, 64, 128, 256]))
+        cases.append((i, g * Hkv, Hkv, Sq, Sk, D, causal, bk))
+    return cases
+
+
+WIDE_CASES = _random_cases_wide(24, 0xD256)
+
+
+@pytest.mark.parametrize("case", WIDE_CASES, ids=["w%02d" % c[0] for c in WIDE_CASES])
+def test_random_shapes_wide(oracle, case):
+    """Seeded random shapes over head dims 130-256, packed short query blocks and many kv
+    heads, against the oracle."""
+    i, Hq, Hkv, Sq, Sk, D, causal, bk = case
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 2000 + i)
+    check(oracle, "wide random %d" % i, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, ref_cap=4)
