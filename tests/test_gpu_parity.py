@@ -239,7 +239,10 @@ def test_head_dim_256(oracle, shape):
     (8, 1, 200, 4096, 128, 1, 0),   # MQA, 1600 rows in 8-wave tiles
     (32, 8, 33, 640, 128, 1, 1),    # V^T input
     (24, 6, 50, 500, 256, 1, 0),    # D = 256
-], ids=["g4-sq17", "g4-sq40", "g16-sq5", "g8-sq100-d96", "mqa-sq200", "vt", "d256"])
+    (32, 8, 40, 20, 128, 1, 0),     # Sq > Sk: each head's first 20 rows attend nothing
+    (16, 1, 60, 7, 64, 1, 0),       # MQA, Sk below one key tile
+], ids=["g4-sq17", "g4-sq40", "g16-sq5", "g8-sq100-d96", "mqa-sq200", "vt", "d256", "sq>sk",
+        "mqa-sk7"])
 def test_gqa_packed_short_queries(oracle, shape):
     Hq, Hkv, Sq, Sk, D, causal, vt = shape
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 700 + Sq)
