@@ -374,6 +374,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 //   * causal: work items are dispatched heaviest first; on grids of at most one workgroup per
 //     CU the key range of each upper-half query tile is split over two workgroups, which write
 //     partials (m, l, acc) for attn_merge2_kernel instead of O.
+//   * short query blocks under GQA (pack): the rows of a kv head's g query heads share query
+//     tiles, each lane carrying its own head and query index.
 // ------------------------------------------------------------------------------------------
 constexpr float kLazyLog2 = 8.0f;
 
