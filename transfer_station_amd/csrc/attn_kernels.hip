@@ -973,29 +973,73 @@ __device__ __forceinline__ size_t merge_orow(long r, int rph, int q_off, int Sq)
     return (size_t)(r / rph) * Sq + q_off + r % rph;
 }
 
-// Any nsplit: one workgroup per partial row, threads across the columns (decode's many splits).
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ pm,
+// Any nsplit up to kMergeMaxSplit: one workgroup of 256 threads per row. The split weights
+// w_s = 2^((m_s - max m) c) / sum_s w_s l_s are computed once, by the whole workgroup, into LDS;
+// then threads take (split group, column) pairs, so the loads of one thread's splits are
+// independent and several groups share a column, and the groups' sums meet in LDS.
+constexpr int kMergeMaxSplit = 512;
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ pm,
                                                          const float *__restrict__ pl,
                                                          const float *__restrict__ pacc,
                                                          float *__restrict__ O, int D, int nsplit,
                                                          float c, int rph, int q_off, int Sq) {
+    __shared__ float wsh[kMergeMaxSplit];
+    __shared__ float red[256];
+    __shared__ float wred[4];
     const long row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const size_t orow = merge_orow(row, rph, q_off, Sq);
     const float *m = pm + row * nsplit;
     const float *l = pl + row * nsplit;
+    auto block_reduce = [&](float v, bool is_max) -> float {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float x = __shfl_xor(v, o);
+            v = is_max ? fmaxf(v, x) : v + x;
+        }
+        if (lane == 0)
+            wred[wv] = v;
+        __syncthreads();
+        const float r = is_max ? fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]))
+                               : (wred[0] + wred[1]) + (wred[2] + wred[3]);
+        __syncthreads();
+        return r;
+    };
     float mx = kNegInf;
-    for (int s = 0; s < nsplit; ++s)
+    for (int s = tid; s < nsplit; s += 256)
         mx = fmaxf(mx, m[s]);
+    mx = block_reduce(mx, true);
     const float muse = (mx == kNegInf) ? 0.f : mx;
-    float lsum = 0.f;
-    for (int s = 0; s < nsplit; ++s)
-        lsum += fast_exp2((m[s] - muse) * c) * l[s];
+    float lpart = 0.f;
+    for (int s = tid; s < nsplit; s += 256) {
+        const float w = fast_exp2((m[s] - muse) * c);
+        wsh[s] = w;
+        lpart += w * l[s];
+    }
+    const float lsum = block_reduce(lpart, false); // its barriers also publish wsh
     const float inv = (lsum > 0.f) ? 1.0f / lsum : 0.f;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float acc = 0.f;
-        for (int s = 0; s < nsplit; ++s)
-            acc += fast_exp2((m[s] - muse) * c) * pacc[((size_t)row * nsplit + s) * D + d];
-        O[orow * D + d] = acc * inv;
+    // sg split groups per column (D <= 256, so sg * D <= 256 threads are busy).
+    const int sg = 256 / D;
+    const int g = tid / D, d = tid - g * D;
+    const float *pr = pacc + (size_t)row * nsplit * D;
+    float acc = 0.f;
+    if (g < sg) {
+        int s = g;
+        for (; s + 3 * sg < nsplit; s += 4 * sg) {
+            const float a0 = pr[(size_t)s * D + d], a1 = pr[(size_t)(s + sg) * D + d];
+            const float a2 = pr[(size_t)(s + 2 * sg) * D + d], a3 = pr[(size_t)(s + 3 * sg) * D + d];
+            acc += wsh[s] * a0 + wsh[s + sg] * a1 + wsh[s + 2 * sg] * a2 + wsh[s + 3 * sg] * a3;
+        }
+        for (; s < nsplit; s += sg)
+            acc += wsh[s] * pr[(size_t)s * D + d];
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (g == 0) {
+        float t = acc;
+        for (int k = 1; k < sg; ++k)
+            t += red[k * D + d];
+        O[orow * D + d] = t * inv;
     }
 }
 
@@ -1122,9 +1166,11 @@ hipError_t launch_merge(const float *pm, const float *pl, const float *pacc, flo
     if (nsplit == 2)
         hipLaunchKernelGGL(attn_merge2_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                            pm, pl, pacc, O, rows, D, c, rph, q_off, Sq);
-    else
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(128), 0, st, pm, pl, pacc,
+    else if (nsplit <= kMergeMaxSplit && D <= 256)
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, pm, pl, pacc,
                            O, D, nsplit, c, rph, q_off, Sq);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
