@@ -493,10 +493,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
 #pragma unroll
     for (int kk = 0; kk < DP / 16; ++kk)
         qb[kk] = as_bf16x8(load_row8<true>(Q, qrow, kk * 16 + hi * 8, D, rvalid));
-    // Q must be resident before the loop: otherwise the compiler's wait at the loop's first
-    // MFMA also waits for the next tile's prefetch (its count cannot tell the two apart).
-    // 0x0F70 = vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding).
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    // Q stays in flight while the first tile's DMA is issued; one wait before the loop covers
+    // both (below).
 
     int nkt = (Sk + KT - 1) / KT;
     int wave_maxkey = wvalid ? Sk - 1 : -1;
@@ -609,7 +607,11 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
 
     if (kt0 < kt1)
         dma_tile(kt0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this wave's DMA blocks have landed
+    // Q and this wave's DMA blocks of the first tile have landed. Q must be resident before
+    // the loop: otherwise the compiler's wait at the loop's first MFMA also waits for the next
+    // tile's prefetch (its count cannot tell the two apart). 0x0F70 = vmcnt(0), expcnt and
+    // lgkmcnt unconstrained (gfx9 encoding).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     for (int kt = kt0; kt < kt1; ++kt) {
         const int buf = (kt - kt0) & 1;
