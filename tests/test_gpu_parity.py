@@ -214,10 +214,10 @@ def test_head_dim_sweep(oracle, D):
     (8, 1, 5, 1001, 192, 1, 128, 0),     # decode row blocks, D = 192
     (8, 2, 300, 640, 256, 1, 128, 1),    # prefill from V^T
     (8, 2, 1, 2048, 256, 0, 128, 1),     # decode from V^T
-    (8, 2, 200, 500, 224, 1, 16, 0),     # 32-key tiles, causal key split, D = 224
+    (8, 2, 200, 500, 224, 1, 16, 0),     # causal key split, D = 224, bk 16
     (6, 3, 130, 70, 200, 1, 128, 0),     # general kernel (D % 8 != 0)
 ], ids=["prefill-causal", "prefill-ragged", "decode", "decode-d192", "prefill-vt", "decode-vt",
-        "kt32-split-d224", "general-d200"])
+        "bk16-split-d224", "general-d200"])
 def test_head_dim_256(oracle, shape):
     Hq, Hkv, Sq, Sk, D, causal, bk, vt = shape
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 256 + Sk)
@@ -316,14 +316,18 @@ def test_key_permutation_invariance(oracle):
     assert oracle.cmp_rows(a, b, Hq, Sq, D, rows)[0]
 
 
-def test_bk_invariance(oracle):
-    Hq, Hkv, Sq, Sk, D = 8, 2, 300, 1000, 128
+@pytest.mark.parametrize("D,Sk", [(128, 1000), (64, 4000), (256, 333), (200, 150)])
+def test_bk_invariance(oracle, D, Sk):
+    """The reference's result is bk-invariant within the tolerance (README:354-357). Here bk is
+    validated and sizes the scratch but never picks the key tile, so O is bit-identical at
+    every bk, on the fast, the D > 128 and the general (D % 8 != 0) kernels alike."""
+    Hq, Hkv, Sq = 8, 2, 300
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 14)
     base = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 1, 128)
-    rows = np.arange(Sq, dtype=np.int32)
+    check(oracle, "bk invariance D=%d" % D, Q, K, V, Hq, Hkv, Sq, Sk, D, 1, 128, ref_cap=8, O=base)
     for bk in (16, 32, 64, 256, 1024, 4096):
         other = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 1, bk)
-        assert oracle.cmp_rows(base, other, Hq, Sq, D, rows)[0], bk
+        assert np.array_equal(base, other), bk
 
 
 # ---- the other entry points ------------------------------------------------------------------------
@@ -364,11 +368,11 @@ VT_CASES = [
     ("fast D128 causal", 8, 2, 513, 1024, 128, 1, 64),
     ("fast D128 kt128 causal", 8, 2, 700, 1000, 128, 1, 128),
     ("fast D64 kt128 causal", 4, 4, 257, 520, 64, 1, 256),
-    ("fast D64 kt32 Sk<KT", 4, 2, 100, 24, 64, 0, 16),
+    ("fast D64 bk16 Sk<KT", 4, 2, 100, 24, 64, 0, 16),
     ("D40 causal Sk%8!=0", 6, 3, 130, 70, 40, 1, 128),
     ("fast D96 causal", 8, 2, 300, 640, 96, 1, 128),
-    ("fast D80 kt64", 8, 4, 200, 512, 80, 0, 64),
-    ("fast D40 kt32", 6, 3, 130, 72, 40, 1, 32),
+    ("fast D80 bk64", 8, 4, 200, 512, 80, 0, 64),
+    ("fast D40 bk32", 6, 3, 130, 72, 40, 1, 32),
     ("general D128 Sk%8!=0", 8, 2, 200, 333, 128, 0, 128),
     ("general D64 Sk%8!=0 causal", 4, 1, 64, 77, 64, 1, 32),
     ("general D7", 4, 2, 40, 50, 7, 0, 64),

@@ -18,7 +18,7 @@
 /* HIP launchers (attn_kernels.hip). Each returns a hipError_t. */
 int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                            int dp, int kt, float c, float *pm, float *pl, float *pacc, long slots,
+                            int dp, float c, float *pm, float *pl, float *pacc, long slots,
                             void *stream);
 int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
@@ -125,17 +125,6 @@ void attn_flash_set_stream(void *stream) { t_stream = stream; }
 void *attn_flash_get_stream(void) { return t_stream; }
 
 /* ---- tile and split selection ------------------------------------------------------------ */
-/* Key-tile size of the prefill kernel for the caller's bk: the online-softmax update runs
- * once per KT keys. bk below 32 (one 32-key MFMA tile) runs at KT=32, bk=64 at 64, and a bk
- * of 128 or more at 128 keys, the largest tile that still fits two waves per SIMD; a larger
- * bk is processed as 128-key sub-blocks, each its own update (the result is bk-invariant
- * within the tolerance, as in the reference). The general (odd-D or unaligned) kernel caps
- * its tile at 64 keys for D > 64. */
-static int attn_kt_for_bk(int bk, int dp) {
-    (void)dp;
-    return (bk <= 32) ? 32 : (bk == 64 ? 64 : 128);
-}
-
 #define ATTN_DECODE_ROWS 16     /* query rows the decode MFMA tile holds (one row block) */
 #define ATTN_DECODE_MAX_ROWS 64 /* g*Sq rows per kv head up to which decode can beat prefill */
 
@@ -191,6 +180,10 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
                 int Hkv, int Sq, int Sk, int D, int causal, int bk, void *scratch,
                 int v_prepacked, struct attn_times *tm) {
     static const char *who = "attn_flash";
+    /* bk keeps the reference's contract (validated here, scratch sized with it), but the key
+     * tile is the hardware's: 128 keys up to D = 128, 64 beyond, whatever bk says. In the
+     * reference bk is a cache-blocking knob whose result is bk-invariant within the tolerance
+     * (README.md:354-357); on the GPU a smaller tile is only slower. */
     attn_bk_check(bk, who);
     attn_d_check(D, who);
     if (Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
@@ -234,8 +227,8 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         struct attn_carve cv;
         attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_prefill(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal ? 1 : 0,
-                                               vec, vt, dp, attn_kt_for_bk(bk, dp), c, cv.m, cv.l,
-                                               cv.acc, ATTN_SLOTS, st),
+                                               vec, vt, dp, c, cv.m, cv.l, cv.acc, ATTN_SLOTS,
+                                               st),
                        who);
     }
     if (tm) {

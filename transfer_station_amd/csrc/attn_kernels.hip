@@ -1314,32 +1314,14 @@ hipError_t launch_prefill_dk(const uint16_t *Q, const uint16_t *K, const uint16_
 template <int DP>
 hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, int causal, int vec, int vt,
-                            int kt, float c, float *pm, float *pl, float *pacc, long slots,
+                            float c, float *pm, float *pl, float *pacc, long slots,
                             hipStream_t st) {
-    // D in (128, 256]: key tiles of at most 64 keys (the fast kernel's two 64-key K and V
-    // tiles fill 128 KB of LDS); the general kernel there always takes 32-key tiles, since its
-    // staging registers and the 256-wide O accumulator leave no room for more.
-    if constexpr (DP == 256) {
-        if (kt <= 32)
-            return launch_prefill_dk<256, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
-                                              pm, pl, pacc, slots, st);
-        return launch_prefill_dk<256, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c, pm,
-                                          pl, pacc, slots, st);
-    } else {
-        switch (kt) {
-        case 32:
-            return launch_prefill_dk<DP, 32>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
-                                             pm, pl, pacc, slots, st);
-        case 64:
-            return launch_prefill_dk<DP, 64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
-                                             pm, pl, pacc, slots, st);
-        case 128:
-            return launch_prefill_dk<DP, 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
-                                              pm, pl, pacc, slots, st);
-        default:
-            return hipErrorInvalidValue;
-        }
-    }
+    // Key tiles of 128 keys up to D = 128, the largest that keeps two waves per SIMD. D in
+    // (128, 256]: 64 keys (the fast kernel's two 64-key K and V tiles fill 128 KB of LDS); the
+    // general kernel there takes 32-key tiles, since its staging registers and the 256-wide O
+    // accumulator leave no room for more.
+    return launch_prefill_dk<DP, DP == 256 ? 64 : 128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec,
+                                                       vt, c, pm, pl, pacc, slots, st);
 }
 
 template <int DP>
@@ -1371,19 +1353,19 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
 // causal key split.
 extern "C" int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                        float *O, int Hq, int Hkv, int Sq, int Sk, int D,
-                                       int causal, int vec, int vt, int dp, int kt, float c,
+                                       int causal, int vec, int vt, int dp, float c,
                                        float *pm, float *pl, float *pacc, long slots,
                                        void *stream) {
     hipStream_t st = (hipStream_t)stream;
     switch (dp) {
     case 64:
-        return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+        return (int)launch_prefill_d<64>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
                                          pm, pl, pacc, slots, st);
     case 128:
-        return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+        return (int)launch_prefill_d<128>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
                                           pm, pl, pacc, slots, st);
     case 256:
-        return (int)launch_prefill_d<256>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, kt, c,
+        return (int)launch_prefill_d<256>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, vec, vt, c,
                                           pm, pl, pacc, slots, st);
     default:
         return (int)hipErrorInvalidValue;
