@@ -1,31 +1,33 @@
-/* flash_cli.c -- TEST HARNESS: the reference's command-line benchmark on one MI355X.
+/* flash_cli.c -- TEST HARNESS: command-line benchmark and self-check of libattn_flash.so.
  *
- * Mirrors the reference's `flash` program (liujiang833/transfer_station flash.c:1177-1321,
- * per-case driver run_case flash.c:1030-1175): same flags, same default suite, same
- * verdict line, same exit codes (0 all pass, 1 a case failed, 2 bad arguments). It drives
- * libattn_flash.so through its C ABI exactly as a C caller of the reference would, and checks
- * every case against the CPU oracle (oracle/attn_oracle.c, the reference's fp32 attn_ref
- * restated), which is why it lives under tests/ and is never part of the library.
+ * Interface kept from the reference's `flash` program (liujiang833/transfer_station,
+ * flash.c:1177-1321 as a specification only): the option names, the default suite's shapes,
+ * the per-case verdict line (flash.c:1151-1156) and the exit status (0 every case passed,
+ * 1 a case failed, 2 the command line was rejected). Scripts that drive the reference's
+ * `flash` therefore drive this program unchanged. The program itself is organised around
+ * three tables: the option table (parser and --help are generated from it), the suite table,
+ * and one `bench` record per case (pool, scratch, check, timing).
  *
- * Differences from the reference harness, each deliberate:
- *   - Buffers are device memory. The cold-input pool holds ncopies copies at distinct
- *     addresses, sized so their total input is >= 2x the cache to overflow (flash.c:982-991);
- *     copy 0 holds the case's LCG data, the others are device-side duplicates of it (what
- *     makes a call cold is the address, not the values), so building the pool costs no host
- *     generation. The pool label reads "hbm" instead of "ddr".
- *   - --llc-mb 0 autodetects the GPU's last-level caches: the L2 the runtime reports plus the
- *     MI355X's 256 MiB Infinity Cache (not reported by the runtime).
- *   - Timing: calls are launched back to back in batches bracketed by HIP events; s/it is
- *     the mean device time per call. The GPU kernel is one fused launch, so the per-phase
- *     split is reported the way attn_times documents it: all of it in qk.
- *   - O is poisoned with NaN before the checked call, so an unwritten row fails.
- *   - --no-softmax is refused (exit 2): a kernel variant that skips work exists only for
- *     profiling experiments, never in the library.
- *   - The default suite is the union of the shipped and the documented suites: the 7
- *     prefill shapes plus the two Sq=1 decode shapes (README.md:524-532).
- *   - Added: --sweep-bk (one shape over every legal bk with one scratch sized for the largest,
- *     README.md:193-216,445-478) and --check-pick-bk (attn_flash_pick_bk's documented
- *     answers and an exact model check, README.md:359-436).
+ * Every case is checked against the CPU oracle (oracle/attn_oracle.c), which is why this
+ * program lives under tests/ and is never part of the library.
+ *
+ * How this harness differs from the reference's, on purpose:
+ *   - Inputs live in device memory. A pool of copies at distinct addresses, together at
+ *     least twice the last-level cache, makes every timed call read cold inputs
+ *     (flash.c:982-991). Copy 0 holds the LCG data; the rest are device-side duplicates, since
+ *     what makes a call cold is its addresses, not its values. The pool is labelled "hbm".
+ *   - --llc-mb 0 sizes the pool from the device: its L2 plus the MI355X's 256 MiB Infinity
+ *     Cache (which the runtime does not report).
+ *   - Times are device times from HIP events around batches of back-to-back calls. One fused
+ *     kernel has no per-phase split, so the line reports all of it as qk (attn_times's rule).
+ *   - O is filled with NaN before the checked call, so a row the kernel never writes fails.
+ *   - --no-softmax is rejected (exit 2). A kernel variant that skips work on purpose is kept
+ *     out of committed code; per-phase cost comes from rocprofv3 counters instead.
+ *   - The default suite adds the two Sq = 1 decode shapes documented in README.md:524-532 to
+ *     the seven shipped prefill shapes.
+ *   - Extra modes: --sweep-bk (one shape at every legal bk, one scratch sized for the largest,
+ *     README.md:193-216,445-478) and --check-pick-bk (attn_flash_pick_bk's documented answers
+ *     plus an exact wide-integer model, README.md:359-436).
  */
 #define _POSIX_C_SOURCE 200809L
 #include "attn_devutil.h"
@@ -39,528 +41,673 @@
 #include <string.h>
 #include <time.h>
 
-static int g_warmup = 3;
-static int g_iters = 0;
-static double g_bench_secs = 0.5;
-static size_t g_llc_bytes = (size_t)512 * 1024 * 1024;
-#define BENCH_MIN_REPS 3
-#define BENCH_DDR_MULT 2u
-#define BENCH_MAX_COPIES 8192
+#define EXIT_ALL_PASS 0
+#define EXIT_CASE_FAILED 1
+#define EXIT_BAD_USAGE 2
+
+#define MIN_TIMED_CALLS 3
+#define POOL_CACHE_MULTIPLE 2u /* pool input bytes >= this many times the cache */
+#define POOL_MAX_COPIES 8192
 #define POOL_ALIGN 256u
-#define INFINITY_CACHE_BYTES ((size_t)256 * 1024 * 1024)
+#define MI355X_INFINITY_CACHE ((size_t)256 << 20)
+#define MAX_BATCH 256
 
-static double now_s(void) {
-    struct timespec t;
-    clock_gettime(CLOCK_MONOTONIC, &t);
-    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
-}
-
-static void hip_or_die(int err, const char *what) {
-    if (err != 0) {
-        printf("HIP error %d in %s\n", err, what);
-        exit(1);
-    }
-}
-
-static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-static size_t detect_llc_bytes(void) {
-    int l2 = 0;
-    if (attn_dev_info(NULL, 0, NULL, 0, NULL, NULL, &l2) != 0 || l2 < 0)
-        l2 = 0;
-    return (size_t)l2 + INFINITY_CACHE_BYTES;
-}
-
-/* Device pool of ncopies input sets: Q, K, V (and V^T when pre-packing) and O per copy. */
-struct pool {
-    int ncopies;
-    size_t q_b, kv_b, o_b, stride;
-    char *base;
+/* ---- configuration, filled by the option table ---------------------------------------------- */
+struct config {
+    int suite_long, prepack_v, sweep, pick_selftest, help, no_softmax;
+    int bk, iters, warmup, llc_mib;
+    double min_secs;
+    const char *shape_text;
 };
 
-static char *pool_at(const struct pool *p, int c, int which) {
-    /* which: 0 Q, 1 K, 2 V, 3 Vp, 4 O */
-    size_t off = (size_t)c * p->stride;
-    size_t q = round_up(p->q_b, POOL_ALIGN), kv = round_up(p->kv_b, POOL_ALIGN);
-    switch (which) {
-    case 0: return p->base + off;
-    case 1: return p->base + off + q;
-    case 2: return p->base + off + q + kv;
-    case 3: return p->base + off + q + 2 * kv;
-    default: return p->base + off + q + 3 * kv;
+static struct config cfg = {
+    .bk = ATTN_BK_DEFAULT, .iters = 0, .warmup = 3, .llc_mib = 512, .min_secs = 0.5,
+};
+
+enum opt_kind { OPT_SWITCH, OPT_INT, OPT_REAL, OPT_TEXT };
+
+struct opt {
+    const char *name;
+    enum opt_kind kind;
+    void *target;
+    const char *metavar; /* shown in --help after the name; NULL for switches */
+    const char *help;    /* lines separated by '\n' */
+};
+
+static const struct opt options[] = {
+    {"--shape", OPT_TEXT, &cfg.shape_text, "Hq,Hkv,Sq,Sk,D[,causal[,ref_cap]]",
+     "one case of this shape instead of the suite (causal 1 and ref_cap 8 when left out;\n"
+     "ref_cap 0 checks every row). Qwen3 1k: --shape 16,8,1024,1024,128,1"},
+    {"--bk", OPT_INT, &cfg.bk, "N",
+     "key-block size passed to attn_flash: a power of two, 16 to 4096 (default 128).\n"
+     "It sizes the scratch; the GPU's key tile does not depend on it, so O is the same"},
+    {"--long", OPT_SWITCH, &cfg.suite_long, NULL,
+     "after the suite, the causal Qwen3 prefill at 1k, 2k and 4k tokens"},
+    {"--prepack-v", OPT_SWITCH, &cfg.prepack_v, NULL,
+     "make V^T once per pool copy with pack_v_full (timed on its own) and call attn_flash\n"
+     "with v_prepacked = 1"},
+    {"--iters", OPT_INT, &cfg.iters, "N", "time exactly N calls per case (0: run by --bench-secs)"},
+    {"--warmup", OPT_INT, &cfg.warmup, "N", "untimed calls before the timed ones (default 3)"},
+    {"--bench-secs", OPT_REAL, &cfg.min_secs, "S",
+     "without --iters: keep timing until S seconds and at least 3 calls (default 0.5)"},
+    {"--llc-mb", OPT_INT, &cfg.llc_mib, "N",
+     "cache size in MiB that the input pool must exceed twice over (default 512;\n"
+     "0: the device's L2 plus its 256 MiB Infinity Cache)"},
+    {"--sweep-bk", OPT_SWITCH, &cfg.sweep, NULL,
+     "time and check one shape (--shape, else 4,2,128,1024,128,0) at every legal bk with a\n"
+     "single scratch sized for bk = 4096"},
+    {"--check-pick-bk", OPT_SWITCH, &cfg.pick_selftest, NULL,
+     "host-only self-test of attn_flash_pick_bk against its documented answers"},
+    {"--no-softmax", OPT_SWITCH, &cfg.no_softmax, NULL,
+     "rejected here (exit 2): no work-skipping kernel variant is built"},
+    {"--help", OPT_SWITCH, &cfg.help, NULL, "print this text"},
+};
+#define NOPTIONS ((int)(sizeof options / sizeof options[0]))
+
+static void print_help(const char *prog) {
+    printf("%s: bf16 flash-attention forward on the GPU, checked against the fp32 CPU oracle\n",
+           prog);
+    printf("Without options it runs the 9-shape suite and prints one verdict line per case.\n\n");
+    for (int i = 0; i < NOPTIONS; i++) {
+        const struct opt *o = &options[i];
+        char head[64];
+        snprintf(head, sizeof head, "%s%s%s", o->name, o->metavar ? " " : "",
+                 o->metavar ? o->metavar : "");
+        const char *line = o->help;
+        int first = 1;
+        while (*line) {
+            const char *nl = strchr(line, '\n');
+            int len = nl ? (int)(nl - line) : (int)strlen(line);
+            if (first && strlen(head) <= 20)
+                printf("  %-20s %.*s\n", head, len, line);
+            else {
+                if (first)
+                    printf("  %s\n", head);
+                printf("  %-20s %.*s\n", "", len, line);
+            }
+            first = 0;
+            line += len + (nl ? 1 : 0);
+        }
     }
+    printf("\nExit status: 0 all cases passed, 1 a case failed, 2 bad command line.\n");
 }
 
-/* Times `fn(arg, i)` on the device: warmup untimed calls, then batches bracketed by HIP events
- * until --iters calls, or >= BENCH_MIN_REPS calls and >= --bench-secs of wall clock. Returns
- * the mean device seconds per call; *reps_o receives the call count. */
-typedef void (*call_fn)(void *arg, int i);
+static const struct opt *find_option(const char *name) {
+    for (int i = 0; i < NOPTIONS; i++)
+        if (strcmp(options[i].name, name) == 0)
+            return &options[i];
+    if (strcmp(name, "-h") == 0)
+        return find_option("--help");
+    return NULL;
+}
 
-static double time_device(call_fn fn, void *arg, int *reps_o) {
-    void *e0 = NULL, *e1 = NULL;
-    hip_or_die(attn_dev_event_create(&e0), "event create");
-    hip_or_die(attn_dev_event_create(&e1), "event create");
-    for (int w = 0; w < g_warmup; w++)
-        fn(arg, w);
-    hip_or_die(attn_dev_synchronize(), "synchronize");
-    int reps = 0, batch = 1;
-    double dev_s = 0.0, t0 = now_s();
-    for (;;) {
-        int n = batch;
-        if (g_iters > 0 && reps + n > g_iters)
-            n = g_iters - reps;
-        hip_or_die(attn_dev_event_record(e0), "event record");
-        for (int i = 0; i < n; i++)
-            fn(arg, reps + i);
-        hip_or_die(attn_dev_event_record(e1), "event record");
-        float ms = 0.f;
-        hip_or_die(attn_dev_event_elapsed_ms(e0, e1, &ms), "event elapsed");
-        dev_s += 1e-3 * (double)ms;
-        reps += n;
-        if (g_iters > 0 ? (reps >= g_iters)
-                        : (reps >= BENCH_MIN_REPS && now_s() - t0 >= g_bench_secs))
+/* Parses a whole decimal number (no trailing text). */
+static int whole_int(const char *s, long *out) {
+    char *end = NULL;
+    long v = strtol(s, &end, 10);
+    if (end == s || *end != '\0')
+        return 0;
+    *out = v;
+    return 1;
+}
+
+/* Returns 1 when argv was understood, else prints why and returns 0. */
+static int parse_args(int argc, char **argv) {
+    for (int i = 1; i < argc; i++) {
+        const struct opt *o = find_option(argv[i]);
+        if (!o) {
+            printf("flash_cli: unrecognised option '%s' (--help lists them)\n", argv[i]);
+            return 0;
+        }
+        if (o->kind == OPT_SWITCH) {
+            *(int *)o->target = 1;
+            continue;
+        }
+        if (i + 1 >= argc) {
+            printf("flash_cli: option %s needs a value (%s)\n", o->name, o->metavar);
+            return 0;
+        }
+        const char *val = argv[++i];
+        if (o->kind == OPT_TEXT) {
+            *(const char **)o->target = val;
+        } else if (o->kind == OPT_INT) {
+            long v;
+            if (!whole_int(val, &v) || v < -2147483647L || v > 2147483647L) {
+                printf("flash_cli: option %s wants an integer, got '%s'\n", o->name, val);
+                return 0;
+            }
+            *(int *)o->target = (int)v;
+        } else {
+            char *end = NULL;
+            double v = strtod(val, &end);
+            if (end == val || *end != '\0') {
+                printf("flash_cli: option %s wants a number, got '%s'\n", o->name, val);
+                return 0;
+            }
+            *(double *)o->target = v;
+        }
+    }
+    return 1;
+}
+
+/* ---- shapes ------------------------------------------------------------------------------- */
+struct shape {
+    const char *label;
+    int Hq, Hkv, Sq, Sk, D, causal, ref_cap;
+};
+
+/* The reference's seven prefill shapes, its two documented decode shapes, and the causal
+ * Qwen3 sweep (16 query heads over 8 kv heads, head dim 128). */
+static const struct shape suite[] = {
+    {"MHA prefill", 4, 4, 8, 8, 64, 0, 0},
+    {"MHA prefil.causal", 4, 4, 8, 8, 64, 1, 0},
+    {"GQA prefill", 8, 2, 8, 8, 64, 0, 0},
+    {"GQA prefil.causal", 8, 2, 8, 8, 64, 1, 0},
+    {"MHA decode(Sq=1)", 4, 4, 1, 16, 64, 0, 0},
+    {"GQA decode(Sq=1)", 8, 2, 1, 16, 64, 0, 0},
+    {"MQA prefill", 8, 1, 8, 8, 64, 0, 0},
+    {"odd + multiblock", 6, 3, 130, 70, 40, 1, 0},
+    {"GQA big head_dim", 8, 2, 4, 12, 128, 0, 0},
+};
+static const struct shape qwen3_sweep[] = {
+    {"qwen3 1k", 16, 8, 1024, 1024, 128, 1, 8},
+    {"qwen3 2k", 16, 8, 2048, 2048, 128, 1, 8},
+    {"qwen3 4k", 16, 8, 4096, 4096, 128, 1, 8},
+};
+#define COUNT(a) ((int)(sizeof(a) / sizeof((a)[0])))
+
+/* --shape text -> shape; 1 on success, else prints the reason and returns 0. */
+static int parse_shape(const char *text, struct shape *s) {
+    long f[7] = {0, 0, 0, 0, 0, 1, 8};
+    int n = 0, dangling = 0;
+    const char *p = text;
+    while (n < 7) {
+        char *end = NULL;
+        f[n] = strtol(p, &end, 10);
+        if (end == p)
             break;
-        if (batch < 256)
-            batch *= 2;
+        n++;
+        dangling = 0;
+        p = end;
+        if (*p != ',')
+            break;
+        p++;
+        dangling = 1;
     }
-    attn_dev_event_destroy(e0);
-    attn_dev_event_destroy(e1);
-    *reps_o = reps;
-    return dev_s / reps;
+    if (n < 5 || dangling || *p != '\0') {
+        printf("flash_cli: --shape wants 5 to 7 comma-separated integers "
+               "Hq,Hkv,Sq,Sk,D[,causal[,ref_cap]], got '%s'\n", text);
+        return 0;
+    }
+    for (int i = 0; i < 7; i++)
+        if (f[i] < -2147483647L || f[i] > 2147483647L) {
+            printf("flash_cli: --shape '%s': a field is out of range\n", text);
+            return 0;
+        }
+    s->label = "custom shape";
+    s->Hq = (int)f[0];
+    s->Hkv = (int)f[1];
+    s->Sq = (int)f[2];
+    s->Sk = (int)f[3];
+    s->D = (int)f[4];
+    s->causal = (int)f[5];
+    s->ref_cap = (int)f[6];
+    if (s->Hq < 1 || s->Hkv < 1 || s->Sq < 1 || s->Sk < 1 || s->D < 1 || s->Hq % s->Hkv != 0) {
+        printf("flash_cli: --shape '%s' rejected: heads, lengths and D must be positive and "
+               "Hq a multiple of Hkv\n", text);
+        return 0;
+    }
+    if (s->D > ATTN_D_MAX) {
+        printf("flash_cli: --shape '%s' rejected: D=%d is above ATTN_D_MAX=%d\n", text, s->D,
+               ATTN_D_MAX);
+        return 0;
+    }
+    if (s->ref_cap < 0) {
+        printf("flash_cli: --shape '%s' rejected: ref_cap must be >= 0\n", text);
+        return 0;
+    }
+    return 1;
 }
 
-struct case_ctx {
-    const struct pool *p;
-    int Hq, Hkv, Sq, Sk, D, causal, bk, prepack_v;
+static int bk_is_legal(int bk) {
+    return bk >= ATTN_BK_MIN && bk <= ATTN_BK_MAX && (bk & (bk - 1)) == 0;
+}
+
+/* ---- device helpers ----------------------------------------------------------------------- */
+static void must(int err, const char *what) {
+    if (err != 0) {
+        printf("flash_cli: HIP error %d during %s\n", err, what);
+        exit(EXIT_CASE_FAILED);
+    }
+}
+
+static double wall_seconds(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+static size_t pad(size_t n) { return (n + POOL_ALIGN - 1) / POOL_ALIGN * POOL_ALIGN; }
+
+/* ---- one case: host data, device pool, scratch -------------------------------------------- */
+enum slot { SLOT_Q, SLOT_K, SLOT_V, SLOT_VT, SLOT_O, NSLOTS };
+
+struct bench {
+    struct shape s;
+    int bk;
+    uint16_t *hq, *hk, *hv; /* host copies of copy 0 (LCG data) for the oracle */
+    size_t nq, nkv;         /* elements */
+    size_t bytes[NSLOTS];
+    size_t offset[NSLOTS];
+    size_t copy_stride;
+    int copies;
+    char *pool;
     void *scratch;
 };
 
-static void call_attn(void *arg, int i) {
-    const struct case_ctx *c = (const struct case_ctx *)arg;
-    int k = i % c->p->ncopies;
-    attn_flash((const uint16_t *)pool_at(c->p, k, 0), (const uint16_t *)pool_at(c->p, k, 1),
-               (const uint16_t *)pool_at(c->p, k, c->prepack_v ? 3 : 2),
-               (float *)pool_at(c->p, k, 4), c->Hq, c->Hkv, c->Sq, c->Sk, c->D, c->causal,
-               c->bk, c->scratch, c->prepack_v, NULL);
+static char *slot_ptr(const struct bench *b, int copy, enum slot s) {
+    return b->pool + (size_t)copy * b->copy_stride + b->offset[s];
 }
 
-static void call_pack(void *arg, int i) {
-    const struct case_ctx *c = (const struct case_ctx *)arg;
-    int k = i % c->p->ncopies;
-    pack_v_full((const uint16_t *)pool_at(c->p, k, 2), (uint16_t *)pool_at(c->p, k, 3), c->Hkv,
-                c->Sk, c->D);
-}
-
-/* Builds the case's data and device pool. Returns 0, or -1 on allocation failure. */
-static int make_case(struct pool *p, uint16_t **Qh, uint16_t **Kh, uint16_t **Vh, int Hq, int Hkv,
-                     int Sq, int Sk, int D) {
-    size_t nq = (size_t)Hq * Sq * D, nk = (size_t)Hkv * Sk * D;
-    *Qh = malloc(nq * 2);
-    *Kh = malloc(nk * 2);
-    *Vh = malloc(nk * 2);
-    if (!*Qh || !*Kh || !*Vh)
+/* Allocates and fills everything a case needs; 0 on success. */
+static int bench_open(struct bench *b, const struct shape *s, int bk, size_t cache_bytes,
+                      size_t scratch_bytes) {
+    memset(b, 0, sizeof *b);
+    b->s = *s;
+    b->bk = bk;
+    b->nq = (size_t)s->Hq * s->Sq * s->D;
+    b->nkv = (size_t)s->Hkv * s->Sk * s->D;
+    b->hq = malloc(b->nq * 2);
+    b->hk = malloc(b->nkv * 2);
+    b->hv = malloc(b->nkv * 2);
+    if (!b->hq || !b->hk || !b->hv)
         return -1;
-    uint32_t rng = 0x12345678u; /* flash.c:1032: every case restarts the generator */
-    attn_synth_lcg_bf16(&rng, *Qh, nq);
-    attn_synth_lcg_bf16(&rng, *Kh, nk);
-    attn_synth_lcg_bf16(&rng, *Vh, nk);
+    /* The reference's data: its LCG restarted at 0x12345678 for every case (flash.c:1030),
+     * drawn Q, then K, then V. */
+    uint32_t state = 0x12345678u;
+    attn_synth_lcg_bf16(&state, b->hq, b->nq);
+    attn_synth_lcg_bf16(&state, b->hk, b->nkv);
+    attn_synth_lcg_bf16(&state, b->hv, b->nkv);
 
-    size_t in_bytes = (nq + 2 * nk) * 2;
-    size_t target = (size_t)BENCH_DDR_MULT * g_llc_bytes;
-    long nc = (long)((target + in_bytes - 1) / in_bytes);
-    if (nc < 1)
-        nc = 1;
-    if (nc > BENCH_MAX_COPIES)
-        nc = BENCH_MAX_COPIES;
-    p->ncopies = (int)nc;
-    p->q_b = nq * 2;
-    p->kv_b = nk * 2;
-    p->o_b = nq * 4;
-    p->stride = round_up(p->q_b, POOL_ALIGN) + 3 * round_up(p->kv_b, POOL_ALIGN) +
-                round_up(p->o_b, POOL_ALIGN);
-    void *base = NULL;
-    if (attn_dev_malloc(&base, p->stride * (size_t)p->ncopies) != 0)
-        return -1;
-    p->base = (char *)base;
-    hip_or_die(attn_dev_memcpy_htod(pool_at(p, 0, 0), *Qh, p->q_b), "upload Q");
-    hip_or_die(attn_dev_memcpy_htod(pool_at(p, 0, 1), *Kh, p->kv_b), "upload K");
-    hip_or_die(attn_dev_memcpy_htod(pool_at(p, 0, 2), *Vh, p->kv_b), "upload V");
-    for (int c = 1; c < p->ncopies; c++) {
-        hip_or_die(attn_dev_memcpy_dtod(pool_at(p, c, 0), pool_at(p, 0, 0), p->q_b), "pool Q");
-        hip_or_die(attn_dev_memcpy_dtod(pool_at(p, c, 1), pool_at(p, 0, 1), p->kv_b), "pool K");
-        hip_or_die(attn_dev_memcpy_dtod(pool_at(p, c, 2), pool_at(p, 0, 2), p->kv_b), "pool V");
+    b->bytes[SLOT_Q] = b->nq * 2;
+    b->bytes[SLOT_K] = b->bytes[SLOT_V] = b->bytes[SLOT_VT] = b->nkv * 2;
+    b->bytes[SLOT_O] = b->nq * 4;
+    size_t off = 0;
+    for (int i = 0; i < NSLOTS; i++) {
+        b->offset[i] = off;
+        off += pad(b->bytes[i]);
     }
+    b->copy_stride = off;
+    const size_t per_call = b->bytes[SLOT_Q] + 2 * b->bytes[SLOT_K];
+    const size_t want = POOL_CACHE_MULTIPLE * cache_bytes;
+    size_t copies = (want + per_call - 1) / per_call;
+    b->copies = (int)(copies < 1 ? 1 : (copies > POOL_MAX_COPIES ? POOL_MAX_COPIES : copies));
+
+    void *p = NULL;
+    if (attn_dev_malloc(&p, b->copy_stride * (size_t)b->copies) != 0)
+        return -1;
+    b->pool = p;
+    must(attn_dev_memcpy_htod(slot_ptr(b, 0, SLOT_Q), b->hq, b->bytes[SLOT_Q]), "upload Q");
+    must(attn_dev_memcpy_htod(slot_ptr(b, 0, SLOT_K), b->hk, b->bytes[SLOT_K]), "upload K");
+    must(attn_dev_memcpy_htod(slot_ptr(b, 0, SLOT_V), b->hv, b->bytes[SLOT_V]), "upload V");
+    for (int c = 1; c < b->copies; c++)
+        for (int sl = SLOT_Q; sl <= SLOT_V; sl++)
+            must(attn_dev_memcpy_dtod(slot_ptr(b, c, sl), slot_ptr(b, 0, sl), b->bytes[sl]),
+                 "pool copy");
+    if (attn_dev_malloc(&b->scratch, scratch_bytes) != 0)
+        return -1;
     return 0;
 }
 
-static void free_case(struct pool *p, uint16_t *Qh, uint16_t *Kh, uint16_t *Vh) {
-    if (p->base)
-        attn_dev_free(p->base);
-    p->base = NULL;
-    free(Qh);
-    free(Kh);
-    free(Vh);
+static void bench_close(struct bench *b) {
+    if (b->scratch)
+        attn_dev_free(b->scratch);
+    if (b->pool)
+        attn_dev_free(b->pool);
+    free(b->hq);
+    free(b->hk);
+    free(b->hv);
+    memset(b, 0, sizeof *b);
 }
 
-/* Correctness of one attn_flash call on copy 0 against the oracle over the spread rows.
- * Returns the pass flag; fills err/scale and the non-finite count. */
-static int check_case(const struct case_ctx *c, const uint16_t *Qh, const uint16_t *Kh,
-                      const uint16_t *Vh, int ref_cap, float *err_o, long *nbad_o, int *nrows_o) {
-    size_t no = (size_t)c->Hq * c->Sq * c->D;
-    float *Oref = calloc(no, 4), *O = malloc(no * 4);
-    int *rows = malloc(sizeof(int) * (size_t)c->Sq);
-    if (!Oref || !O || !rows) {
-        printf("host allocation failed\n");
-        exit(1);
+static void call_attention(const struct bench *b, int i) {
+    const int c = i % b->copies;
+    const struct shape *s = &b->s;
+    attn_flash((const uint16_t *)slot_ptr(b, c, SLOT_Q), (const uint16_t *)slot_ptr(b, c, SLOT_K),
+               (const uint16_t *)slot_ptr(b, c, cfg.prepack_v ? SLOT_VT : SLOT_V),
+               (float *)slot_ptr(b, c, SLOT_O), s->Hq, s->Hkv, s->Sq, s->Sk, s->D, s->causal,
+               b->bk, b->scratch, cfg.prepack_v, NULL);
+}
+
+static void call_pack(const struct bench *b, int i) {
+    const int c = i % b->copies;
+    pack_v_full((const uint16_t *)slot_ptr(b, c, SLOT_V), (uint16_t *)slot_ptr(b, c, SLOT_VT),
+                b->s.Hkv, b->s.Sk, b->s.D);
+}
+
+/* Mean device seconds per call of `op`: warmup calls, then batches (doubling up to MAX_BATCH)
+ * between two HIP events, until --iters calls or, without it, MIN_TIMED_CALLS calls and
+ * --bench-secs of wall time. */
+struct timing {
+    double per_call;
+    int calls;
+};
+
+static struct timing measure(const struct bench *b, void (*op)(const struct bench *, int)) {
+    void *start = NULL, *stop = NULL;
+    must(attn_dev_event_create(&start), "event");
+    must(attn_dev_event_create(&stop), "event");
+    for (int i = 0; i < cfg.warmup; i++)
+        op(b, i);
+    must(attn_dev_synchronize(), "warmup");
+    struct timing t = {0.0, 0};
+    double device_s = 0.0;
+    const double t0 = wall_seconds();
+    for (int batch = 1;; batch = batch < MAX_BATCH ? 2 * batch : MAX_BATCH) {
+        if (cfg.iters > 0 && t.calls + batch > cfg.iters)
+            batch = cfg.iters - t.calls;
+        must(attn_dev_event_record(start), "event record");
+        for (int i = 0; i < batch; i++)
+            op(b, t.calls + i);
+        must(attn_dev_event_record(stop), "event record");
+        float ms = 0.f;
+        must(attn_dev_event_elapsed_ms(start, stop, &ms), "event time");
+        device_s += (double)ms * 1e-3;
+        t.calls += batch;
+        const int done = cfg.iters > 0
+                             ? t.calls >= cfg.iters
+                             : (t.calls >= MIN_TIMED_CALLS && wall_seconds() - t0 >= cfg.min_secs);
+        if (done)
+            break;
     }
-    int nrows = orc_ref_rowset(c->Sq, ref_cap, rows);
-    orc_attn_ref_mt(Qh, Kh, Vh, Oref, c->Hq, c->Hkv, c->Sq, c->Sk, c->D, c->causal, rows, nrows,
-                    0);
-    hip_or_die(attn_dev_memset(pool_at(c->p, 0, 4), 0xFF, c->p->o_b), "poison O");
-    call_attn((void *)c, 0);
-    hip_or_die(attn_dev_synchronize(), "synchronize");
-    hip_or_die(attn_dev_memcpy_dtoh(O, pool_at(c->p, 0, 4), no * 4), "download O");
+    attn_dev_event_destroy(start);
+    attn_dev_event_destroy(stop);
+    t.per_call = device_s / t.calls;
+    return t;
+}
+
+/* Checked call on copy 0 against the oracle over the spread rows (ref_cap, flash.c:900-913). */
+struct check {
+    int pass, rows;
+    long nonfinite;
+    float err_scale;
+};
+
+static struct check verify(const struct bench *b) {
+    const struct shape *s = &b->s;
+    struct check r = {0, 0, 0, 0.f};
+    float *want = calloc(b->nq, sizeof(float)), *got = malloc(b->nq * sizeof(float));
+    int *rows = malloc(sizeof(int) * (size_t)s->Sq);
+    if (!want || !got || !rows) {
+        printf("flash_cli: host memory exhausted\n");
+        exit(EXIT_CASE_FAILED);
+    }
+    r.rows = orc_ref_rowset(s->Sq, s->ref_cap, rows);
+    orc_attn_ref_mt(b->hq, b->hk, b->hv, want, s->Hq, s->Hkv, s->Sq, s->Sk, s->D, s->causal,
+                    rows, r.rows, 0);
+    must(attn_dev_memset(slot_ptr(b, 0, SLOT_O), 0xFF, b->bytes[SLOT_O]), "poison O");
+    call_attention(b, 0);
+    must(attn_dev_synchronize(), "checked call");
+    must(attn_dev_memcpy_dtoh(got, slot_ptr(b, 0, SLOT_O), b->bytes[SLOT_O]), "download O");
     float mad = 0.f, maxref = 0.f;
-    long nbad = 0;
-    int ok = orc_cmp_rows(Oref, O, c->Hq, c->Sq, c->D, rows, nrows, &mad, &maxref, &nbad);
-    *err_o = maxref > 0 ? mad / maxref : 0.f;
-    *nbad_o = nbad;
-    *nrows_o = nrows;
-    free(Oref);
-    free(O);
+    r.pass = orc_cmp_rows(want, got, s->Hq, s->Sq, s->D, rows, r.rows, &mad, &maxref,
+                          &r.nonfinite);
+    r.err_scale = maxref > 0.f ? mad / maxref : 0.f;
+    free(want);
+    free(got);
     free(rows);
-    return ok;
+    return r;
 }
 
-static int run_case(const char *name, int Hq, int Hkv, int Sq, int Sk, int D, int causal,
-                    int ref_cap, int bk, int prepack_v) {
-    struct pool p = {0};
-    uint16_t *Qh = NULL, *Kh = NULL, *Vh = NULL;
-    if (make_case(&p, &Qh, &Kh, &Vh, Hq, Hkv, Sq, Sk, D) != 0) {
-        printf("%-17s allocation failed\n", name);
-        free_case(&p, Qh, Kh, Vh);
-        return 0;
-    }
-    void *scratch = NULL;
-    hip_or_die(attn_dev_malloc(&scratch, attn_flash_scratch_bytes(D, bk)), "scratch");
-    struct case_ctx c = {&p, Hq, Hkv, Sq, Sk, D, causal, bk, prepack_v, scratch};
+static double useful_gflop(const struct shape *s) {
+    return 4.0 * (double)s->Hq * (double)s->D * orc_attn_pairs(s->Sq, s->Sk, s->causal) * 1e-9;
+}
 
-    double tpack = 0.0;
-    if (prepack_v) {
-        for (int k = 0; k < p.ncopies; k++)
-            call_pack(&c, k);
-        int preps = 0;
-        tpack = time_device(call_pack, &c, &preps);
-    }
-    float err = 0.f;
-    long nbad = 0;
-    int nrows = 0;
-    int ok = check_case(&c, Qh, Kh, Vh, ref_cap, &err, &nbad, &nrows);
-
-    int reps = 0;
-    double tdot = time_device(call_attn, &c, &reps);
-
-    char reflbl[48] = "";
-    if (nrows < Sq)
-        snprintf(reflbl, sizeof reflbl, " [ref:%d rows spread 0..%d]", nrows, Sq - 1);
-    char verdict[40];
-    if (nbad)
-        snprintf(verdict, sizeof verdict, "*** FAIL (%ld non-finite) ***", nbad);
+/* The verdict line: field order and format are the reference's (flash.c:1151-1156), with the
+ * pool labelled "hbm" and per-phase times as attn_times reports them (all in qk). */
+static void report(const struct bench *b, const struct check *ck, const struct timing *t,
+                   double pack_s) {
+    const struct shape *s = &b->s;
+    char rowsnote[48] = "", packnote[40] = "", verdict[40];
+    if (ck->rows < s->Sq)
+        snprintf(rowsnote, sizeof rowsnote, " [ref:%d rows spread 0..%d]", ck->rows, s->Sq - 1);
+    if (cfg.prepack_v)
+        snprintf(packnote, sizeof packnote, " sep-packv=%.6fs", pack_s);
+    if (ck->nonfinite)
+        snprintf(verdict, sizeof verdict, "*** FAIL (%ld non-finite) ***", ck->nonfinite);
     else
-        snprintf(verdict, sizeof verdict, "%s", ok ? "PASS" : "*** FAIL ***");
-    char packlbl[40] = "";
-    if (prepack_v)
-        snprintf(packlbl, sizeof packlbl, " sep-packv=%.6fs", tpack);
-    double gflop = 4.0 * (double)Hq * D * orc_attn_pairs(Sq, Sk, causal) / 1e9;
-    double pool_mib = (double)p.ncopies * (double)(p.q_b + 2 * p.kv_b) / (1024.0 * 1024.0);
+        snprintf(verdict, sizeof verdict, "%s", ck->pass ? "PASS" : "*** FAIL ***");
+    const double gf = useful_gflop(s);
+    const double pool_mib =
+        (double)b->copies * (double)(b->bytes[SLOT_Q] + 2 * b->bytes[SLOT_K]) / 1048576.0;
     printf("%-17s H=%2d/%-2d(g%d) Sq=%-4d Sk=%-4d D=%3d bk=%-4d %s | err/scale=%.1e | %7.2f GFLOP "
            "%11.6fs/it x%-5d %9.2f GFLOP/s | pv/qk/sm/sv=%.6f/%.6f/%.6f/%.6f | hbm %dx=%.0fMiB%s%s "
            "-> %s\n",
-           name, Hq, Hkv, Hq / Hkv, Sq, Sk, D, bk, causal ? "causal" : "full  ", err, gflop, tdot,
-           reps, gflop / tdot, 0.0, tdot, 0.0, 0.0, p.ncopies, pool_mib, packlbl, reflbl,
+           s->label, s->Hq, s->Hkv, s->Hq / s->Hkv, s->Sq, s->Sk, s->D, b->bk,
+           s->causal ? "causal" : "full  ", ck->err_scale, gf, t->per_call, t->calls,
+           gf / t->per_call, 0.0, t->per_call, 0.0, 0.0, b->copies, pool_mib, packnote, rowsnote,
            verdict);
     fflush(stdout);
-    attn_dev_free(scratch);
-    free_case(&p, Qh, Kh, Vh);
-    return ok;
 }
 
-/* One shape over every legal bk, with ONE scratch sized for the largest bk and poisoned
- * first (README.md:193-216): each bk checked against the oracle and timed. Prints the
- * fastest bk next to attn_flash_pick_bk's analytic answer for the device's L2. */
-static int sweep_bk(int Hq, int Hkv, int Sq, int Sk, int D, int causal, int ref_cap,
-                    int prepack_v) {
-    struct pool p = {0};
-    uint16_t *Qh = NULL, *Kh = NULL, *Vh = NULL;
-    if (make_case(&p, &Qh, &Kh, &Vh, Hq, Hkv, Sq, Sk, D) != 0) {
-        printf("sweep: allocation failed\n");
-        free_case(&p, Qh, Kh, Vh);
+static size_t g_cache_bytes;
+
+/* Pack every copy's V^T (so each timed call reads its own), then time the pack itself. */
+static double prepare_vt(const struct bench *b) {
+    if (!cfg.prepack_v)
+        return 0.0;
+    for (int c = 0; c < b->copies; c++)
+        call_pack(b, c);
+    return measure(b, call_pack).per_call;
+}
+
+static int run_one(const struct shape *s) {
+    struct bench b;
+    if (bench_open(&b, s, cfg.bk, g_cache_bytes, attn_flash_scratch_bytes(s->D, cfg.bk)) != 0) {
+        printf("%-17s could not allocate its buffers\n", s->label);
+        bench_close(&b);
         return 0;
     }
-    const size_t sbytes = attn_flash_scratch_bytes(D, ATTN_BK_MAX);
-    void *scratch = NULL;
-    hip_or_die(attn_dev_malloc(&scratch, sbytes), "scratch");
-    hip_or_die(attn_dev_memset(scratch, 0xFF, sbytes), "poison scratch");
-    double gflop = 4.0 * (double)Hq * D * orc_attn_pairs(Sq, Sk, causal) / 1e9;
-    printf("--- bk sweep: Hq=%d Hkv=%d Sq=%d Sk=%d D=%d %s, one scratch of %zu B (sized for "
-           "bk=%d) ---\n",
-           Hq, Hkv, Sq, Sk, D, causal ? "causal" : "full", sbytes, ATTN_BK_MAX);
+    const double pack_s = prepare_vt(&b);
+    const struct check ck = verify(&b);
+    const struct timing t = measure(&b, call_attention);
+    report(&b, &ck, &t, pack_s);
+    bench_close(&b);
+    return ck.pass;
+}
+
+/* ---- --sweep-bk ----------------------------------------------------------------------------- */
+/* One scratch sized for the largest bk and poisoned first serves every bk (the size is
+ * non-decreasing in bk, README.md:193-216). bk does not select the GPU's key tile, so every
+ * row runs the same kernel: the sweep shows that the result and the time do not depend on bk. */
+static int sweep_bk(const struct shape *s) {
+    struct bench b;
+    const size_t big = attn_flash_scratch_bytes(s->D, ATTN_BK_MAX);
+    if (bench_open(&b, s, ATTN_BK_MAX, g_cache_bytes, big) != 0) {
+        printf("sweep: could not allocate its buffers\n");
+        bench_close(&b);
+        return 0;
+    }
+    must(attn_dev_memset(b.scratch, 0xFF, big), "poison scratch");
+    printf("--- bk sweep: Hq=%d Hkv=%d Sq=%d Sk=%d D=%d %s; one %zu-byte scratch (bk=%d size) "
+           "serves every bk ---\n",
+           s->Hq, s->Hkv, s->Sq, s->Sk, s->D, s->causal ? "causal" : "full", big, ATTN_BK_MAX);
+    printf("note: the key tile is fixed by D, so every bk runs the same kernel\n");
     printf("%6s %10s %12s %12s %10s  %s\n", "bk", "scratch B", "err/scale", "s/it", "GFLOP/s",
            "verdict");
-    int all = 1, best_bk = 0;
-    double best_t = 0.0;
-    struct case_ctx c = {&p, Hq, Hkv, Sq, Sk, D, causal, 0, prepack_v, scratch};
-    if (prepack_v)
-        for (int k = 0; k < p.ncopies; k++)
-            call_pack(&c, k);
-    for (int bk = ATTN_BK_MIN; bk <= ATTN_BK_MAX; bk *= 2) {
-        c.bk = bk;
-        float err = 0.f;
-        long nbad = 0;
-        int nrows = 0;
-        int ok = check_case(&c, Qh, Kh, Vh, ref_cap, &err, &nbad, &nrows);
-        int reps = 0;
-        double t = time_device(call_attn, &c, &reps);
-        printf("%6d %10zu %12.1e %12.6f %10.1f  %s\n", bk, attn_flash_scratch_bytes(D, bk), err, t,
-               gflop / t, ok ? "PASS" : "*** FAIL ***");
+    prepare_vt(&b);
+    const double gf = useful_gflop(s);
+    int all = 1;
+    double tmin = 0.0, tmax = 0.0;
+    for (int bk = ATTN_BK_MIN; bk <= ATTN_BK_MAX; bk <<= 1) {
+        b.bk = bk;
+        const struct check ck = verify(&b);
+        const struct timing t = measure(&b, call_attention);
+        printf("%6d %10zu %12.1e %12.6f %10.1f  %s\n", bk, attn_flash_scratch_bytes(s->D, bk),
+               ck.err_scale, t.per_call, gf / t.per_call, ck.pass ? "PASS" : "*** FAIL ***");
         fflush(stdout);
-        all &= ok;
-        if (best_bk == 0 || t < best_t) {
-            best_bk = bk;
-            best_t = t;
-        }
+        all = all && ck.pass;
+        tmin = (bk == ATTN_BK_MIN || t.per_call < tmin) ? t.per_call : tmin;
+        tmax = (bk == ATTN_BK_MIN || t.per_call > tmax) ? t.per_call : tmax;
     }
     int l2 = 0;
     attn_dev_info(NULL, 0, NULL, 0, NULL, NULL, &l2);
-    printf("fastest bk=%d (%.6f s/it); attn_flash_pick_bk(D=%d, L2=%d B) = %d (analytic model)\n",
-           best_bk, best_t, D, l2, attn_flash_pick_bk(D, (size_t)(l2 > 0 ? l2 : 0)));
-    attn_dev_free(scratch);
-    free_case(&p, Qh, Kh, Vh);
+    printf("spread over bk: %.1f%% (one kernel; run-to-run noise). attn_flash_pick_bk(D=%d, "
+           "L2=%d B) = %d from the reference's cache model\n",
+           tmin > 0 ? 100.0 * (tmax - tmin) / tmin : 0.0, s->D, l2,
+           attn_flash_pick_bk(s->D, (size_t)(l2 > 0 ? l2 : 0)));
+    bench_close(&b);
     return all;
 }
 
-/* attn_flash_pick_bk self-test (README.md:359-436): the documented answers, the worked
- * example's bound, the edge cases, and an exact 128-bit restatement of the model over a grid
- * of (D, l2). Host only. */
-static int pick_model_exact(long long D, unsigned long long l2) {
-    const unsigned __int128 BQm = 64;
-    unsigned __int128 d = D < 1 ? 1 : (unsigned __int128)D;
-    unsigned __int128 per_bk = 6 * (d + BQm), fixed = 6 * BQm * d + 4 * d + 12 * BQm;
+/* ---- --check-pick-bk (host only) ------------------------------------------------------------ */
+/* The cache model restated in 128-bit arithmetic, where nothing can overflow. */
+static int pick_exact(long long D, unsigned long long l2) {
+    typedef unsigned __int128 u128;
+    const u128 rows = 64, d = D < 1 ? 1 : (u128)D;
     int best = ATTN_BK_MIN;
-    for (int bk = ATTN_BK_MIN; bk <= ATTN_BK_MAX; bk *= 2) {
-        if (2 * (per_bk * (unsigned __int128)bk + fixed) > (unsigned __int128)l2)
+    for (int bk = ATTN_BK_MIN; bk <= ATTN_BK_MAX; bk <<= 1) {
+        const u128 ws = 6 * (u128)bk * (d + rows) + 6 * rows * d + 4 * d + 12 * rows;
+        if (2 * ws > (u128)l2)
             break;
         best = bk;
     }
     return best;
 }
 
-static int check_pick_bk(void) {
-    int fails = 0;
-#define EXPECT(cond, ...)                                                                          \
-    do {                                                                                           \
-        if (!(cond)) {                                                                             \
-            fails++;                                                                               \
-            printf("  FAIL: " __VA_ARGS__);                                                        \
-            printf("\n");                                                                          \
-        }                                                                                          \
-    } while (0)
-    const int want_l2[4] = {256, 512, 1024, 2048};
-    for (int i = 0; i < 4; i++) {
-        int got = attn_flash_pick_bk(128, ((size_t)1 << 20) << i);
-        EXPECT(got == want_l2[i], "pick_bk(128, %d MiB) = %d, documented %d", 1 << i, got,
-               want_l2[i]);
+static int pick_failures;
+static void expect(int ok, const char *what) {
+    if (!ok) {
+        pick_failures++;
+        printf("  FAIL: %s\n", what);
     }
-    const int dd[4] = {64, 128, 256, 512}, want_d[4] = {512, 256, 128, 64};
-    for (int i = 0; i < 4; i++) {
-        int got = attn_flash_pick_bk(dd[i], (size_t)1 << 20);
-        EXPECT(got == want_d[i], "pick_bk(%d, 1 MiB) = %d, documented %d", dd[i], got, want_d[i]);
-    }
-    /* worked example: 2*(1152*bk + 50432) <= 2^20 holds at 256 and fails at 512 */
-    EXPECT(2.0 * (1152.0 * 256 + 50432.0) <= 1048576.0, "bound at bk=256");
-    EXPECT(2.0 * (1152.0 * 512 + 50432.0) > 1048576.0, "bound at bk=512");
-    EXPECT(attn_flash_pick_bk(128, 0) == ATTN_BK_MIN, "l2=0 must give the floor");
-    EXPECT(attn_flash_pick_bk(128, SIZE_MAX) == ATTN_BK_MAX, "l2=SIZE_MAX must give the cap");
-    EXPECT(attn_flash_pick_bk(0, 1 << 20) == attn_flash_pick_bk(1, 1 << 20), "D<1 clamps to 1");
-    EXPECT(attn_flash_pick_bk(-5, 1 << 20) == attn_flash_pick_bk(1, 1 << 20), "D<1 clamps to 1");
-    const long long Ds[] = {1, 2, 40, 64, 100, 128, 256, 1024, 65536, 1LL << 24, 2147483647LL};
-    const unsigned long long L2s[] = {0ull, 1ull, 4096ull, 1ull << 20, 3ull << 20, 1ull << 22,
-                                      256ull << 20, 1ull << 40, 2000000000000ull,
-                                      18446744073709551615ull};
-    int checked = 0;
-    for (size_t i = 0; i < sizeof Ds / sizeof Ds[0]; i++)
-        for (size_t j = 0; j < sizeof L2s / sizeof L2s[0]; j++) {
-            int got = attn_flash_pick_bk((int)Ds[i], (size_t)L2s[j]);
-            int want = pick_model_exact(Ds[i], L2s[j]);
-            EXPECT(got == want, "pick_bk(%lld, %llu) = %d, exact model %d", Ds[i], L2s[j], got,
-                   want);
-            EXPECT(got >= ATTN_BK_MIN && got <= ATTN_BK_MAX && (got & (got - 1)) == 0,
-                   "pick_bk(%lld, %llu) = %d is not a power of two in range", Ds[i], L2s[j], got);
-            checked++;
-        }
-#undef EXPECT
-    printf("PICK_BK %s, %d checks failed (%d exact-model combinations)\n", fails ? "FAILED" : "OK",
-           fails, checked);
-    return fails == 0;
 }
 
-static void usage(const char *argv0) {
-    printf("usage: %s [--long] [--shape Hq,Hkv,Sq,Sk,D[,causal[,ref_cap]]] [--bk N]\n", argv0);
-    printf("       %*s [--prepack-v] [--iters N] [--warmup N] [--bench-secs S] [--llc-mb N]\n",
-           (int)strlen(argv0), "");
-    printf("       %*s [--sweep-bk] [--check-pick-bk]\n", (int)strlen(argv0), "");
-    printf("  (no args)       run the default suite (7 prefill + 2 decode shapes)\n");
-    printf("  --shape ...     run ONE case of the given shape instead of the suite, then exit;\n");
-    printf("                  causal defaults to 1, ref_cap to 8. Qwen3 1k prefill, on its own:\n");
-    printf("                  --shape 16,8,1024,1024,128,1\n");
-    printf("  --bk N          key-block size N (power of two in [%d,%d]); default %d. RUNTIME.\n",
-           ATTN_BK_MIN, ATTN_BK_MAX, ATTN_BK_DEFAULT);
-    printf("  --long          also run the Qwen3 1k/2k/4k prefill sweep\n");
-    printf("  --prepack-v     transpose V with the SEPARATE pack_v_full operator before attention\n");
-    printf("                  (attn_flash runs v_prepacked=1)\n");
-    printf("  --iters N       time exactly N runs per case (default: adaptive to --bench-secs)\n");
-    printf("  --warmup N      untimed warmup runs before timing (default 3)\n");
-    printf("  --bench-secs S  adaptive: keep timing a case until S seconds elapse (default 0.5)\n");
-    printf("  --llc-mb N      cache (MiB) the input pool must overflow so calls stream from HBM\n");
-    printf("                  (default 512; 0 = the device's L2 + 256 MiB Infinity Cache)\n");
-    printf("  --sweep-bk      one shape (--shape, default 4,2,128,1024,128,0) over every legal\n");
-    printf("                  bk with one scratch sized for bk=%d; prints the fastest bk\n",
-           ATTN_BK_MAX);
-    printf("  --check-pick-bk self-test attn_flash_pick_bk's cache model (host only)\n");
-    printf("  --no-softmax    not available in this build (exits 2)\n");
+static int pick_selftest(void) {
+    char msg[160];
+    /* Documented answers: D = 128 over 1/2/4/8 MiB, and four D at 1 MiB. */
+    static const struct { int D; size_t l2; int want; } known[] = {
+        {128, 1u << 20, 256}, {128, 2u << 20, 512}, {128, 4u << 20, 1024}, {128, 8u << 20, 2048},
+        {64, 1u << 20, 512},  {256, 1u << 20, 128}, {512, 1u << 20, 64},
+    };
+    for (int i = 0; i < COUNT(known); i++) {
+        const int got = attn_flash_pick_bk(known[i].D, known[i].l2);
+        snprintf(msg, sizeof msg, "pick_bk(%d, %zu) = %d, documented %d", known[i].D, known[i].l2,
+                 got, known[i].want);
+        expect(got == known[i].want, msg);
+    }
+    /* The worked example's bound for D = 128 at 1 MiB: 2*(1152*bk + 50432) fits at 256 only. */
+    expect(2 * (1152L * 256 + 50432) <= (1L << 20), "worked example holds at bk = 256");
+    expect(2 * (1152L * 512 + 50432) > (1L << 20), "worked example fails at bk = 512");
+    expect(attn_flash_pick_bk(128, 0) == ATTN_BK_MIN, "an empty cache gives the floor");
+    expect(attn_flash_pick_bk(128, SIZE_MAX) == ATTN_BK_MAX, "SIZE_MAX gives the cap");
+    expect(attn_flash_pick_bk(0, 1u << 20) == attn_flash_pick_bk(1, 1u << 20), "D = 0 acts as 1");
+    expect(attn_flash_pick_bk(-5, 1u << 20) == attn_flash_pick_bk(1, 1u << 20), "D < 0 acts as 1");
+    static const long long dims[] = {1, 2, 40, 64, 100, 128, 256, 1024, 65536, 1LL << 24,
+                                     2147483647LL};
+    static const unsigned long long caches[] = {
+        0ull, 1ull, 4096ull, 1ull << 20, 3ull << 20, 1ull << 22, 256ull << 20, 1ull << 40,
+        2000000000000ull, 18446744073709551615ull};
+    int combos = 0;
+    for (int i = 0; i < COUNT(dims); i++)
+        for (int j = 0; j < COUNT(caches); j++, combos++) {
+            const int got = attn_flash_pick_bk((int)dims[i], (size_t)caches[j]);
+            const int want = pick_exact(dims[i], caches[j]);
+            snprintf(msg, sizeof msg, "pick_bk(%lld, %llu) = %d, exact model %d", dims[i],
+                     caches[j], got, want);
+            expect(got == want && bk_is_legal(got), msg);
+        }
+    printf("PICK_BK %s, %d checks failed (%d exact-model combinations)\n",
+           pick_failures ? "FAILED" : "OK", pick_failures, combos);
+    return pick_failures == 0;
+}
+
+/* ---- main ----------------------------------------------------------------------------------- */
+static void print_banner(void) {
+    char name[128] = "", arch[64] = "";
+    int cus = 0, khz = 0, l2 = 0;
+    attn_dev_info(name, sizeof name, arch, sizeof arch, &cus, &khz, &l2);
+    printf("=== FLASH bf16 attention (online softmax, gfx950 MFMA vs fp32 ref) ===\n");
+    printf("device %s [%s]: %d CUs, %d MHz, L2 %d KiB\n", name, arch, cus, khz / 1000, l2 / 1024);
+    printf("bk=%d (a runtime argument; scratch %zu B at D=128). V enters as %s\n", cfg.bk,
+           attn_flash_scratch_bytes(128, cfg.bk),
+           cfg.prepack_v ? "V^T from pack_v_full (v_prepacked=1)"
+                         : "row-major V (transposed on LDS reads)");
+    if (cfg.iters > 0)
+        printf("timing: %d warmup calls, then %d timed calls per case", cfg.warmup, cfg.iters);
+    else
+        printf("timing: %d warmup calls, then at least %d calls and %.2g s per case", cfg.warmup,
+               MIN_TIMED_CALLS, cfg.min_secs);
+    printf("; s/it is mean device time (HIP events). Inputs rotate over a pool >= %ux %.1f MiB, "
+           "shown as 'hbm copies x MiB'. pv/qk/sm/sv: one fused kernel, so all time is in qk\n",
+           POOL_CACHE_MULTIPLE, (double)g_cache_bytes / 1048576.0);
 }
 
 int main(int argc, char **argv) {
-    int longrun = 0, prepack_v = 0, bk = ATTN_BK_DEFAULT, sweep = 0, pickcheck = 0;
-    int shq = 0, shkv = 0, ssq = 0, ssk = 0, sd = 0, scausal = 1, srefcap = 8, have_shape = 0;
     setvbuf(stdout, NULL, _IOLBF, 0);
-    for (int i = 1; i < argc; i++) {
-        if (!strcmp(argv[i], "--long"))
-            longrun = 1;
-        else if (!strcmp(argv[i], "--prepack-v"))
-            prepack_v = 1;
-        else if (!strcmp(argv[i], "--sweep-bk"))
-            sweep = 1;
-        else if (!strcmp(argv[i], "--check-pick-bk"))
-            pickcheck = 1;
-        else if (!strcmp(argv[i], "--no-softmax")) {
-            printf("--no-softmax: not available. This build keeps no work-skipping kernel "
-                   "variant; per-phase attribution comes from rocprofv3 counters instead.\n");
-            return 2;
-        } else if (!strcmp(argv[i], "--bk") && i + 1 < argc)
-            bk = atoi(argv[++i]);
-        else if (!strcmp(argv[i], "--shape") && i + 1 < argc) {
-            scausal = 1;
-            srefcap = 8;
-            int n = sscanf(argv[++i], "%d,%d,%d,%d,%d,%d,%d", &shq, &shkv, &ssq, &ssk, &sd,
-                           &scausal, &srefcap);
-            if (n < 5) {
-                printf("bad --shape: need Hq,Hkv,Sq,Sk,D[,causal[,ref_cap]]\n");
-                return 2;
-            }
-            have_shape = 1;
-        } else if (!strcmp(argv[i], "--iters") && i + 1 < argc)
-            g_iters = atoi(argv[++i]);
-        else if (!strcmp(argv[i], "--warmup") && i + 1 < argc)
-            g_warmup = atoi(argv[++i]);
-        else if (!strcmp(argv[i], "--bench-secs") && i + 1 < argc)
-            g_bench_secs = atof(argv[++i]);
-        else if (!strcmp(argv[i], "--llc-mb") && i + 1 < argc) {
-            size_t mb = strtoul(argv[++i], NULL, 10);
-            g_llc_bytes = mb ? mb * 1024u * 1024u : 0; /* 0: autodetect once a device is up */
-        } else if (!strcmp(argv[i], "--help") || !strcmp(argv[i], "-h")) {
-            usage(argv[0]);
-            return 0;
-        } else {
-            printf("unknown argument: %s\n", argv[i]);
-            usage(argv[0]);
-            return 2;
-        }
+    if (!parse_args(argc, argv))
+        return EXIT_BAD_USAGE;
+    if (cfg.help) {
+        print_help(argv[0]);
+        return EXIT_ALL_PASS;
     }
-    if (bk < ATTN_BK_MIN || bk > ATTN_BK_MAX || (bk & (bk - 1)) != 0) {
-        printf("bad --bk %d: must be a power of two in [%d, %d]\n", bk, ATTN_BK_MIN, ATTN_BK_MAX);
-        return 2;
+    if (cfg.no_softmax) {
+        printf("flash_cli: --no-softmax is rejected: this build ships no kernel variant that "
+               "skips work; measure phases with rocprofv3 counters instead\n");
+        return EXIT_BAD_USAGE;
     }
-    if (have_shape && (shq < 1 || shkv < 1 || shq % shkv != 0 || ssq < 1 || ssk < 1 || sd < 1)) {
-        printf("bad --shape %d,%d,%d,%d,%d: need Hq>=1, Hkv>=1, Hq%%Hkv==0, Sq>=1, Sk>=1, D>=1\n",
-               shq, shkv, ssq, ssk, sd);
-        return 2;
+    if (!bk_is_legal(cfg.bk)) {
+        printf("flash_cli: --bk %d rejected: bk must be a power of two from %d to %d\n", cfg.bk,
+               ATTN_BK_MIN, ATTN_BK_MAX);
+        return EXIT_BAD_USAGE;
     }
-    if (have_shape && sd > ATTN_D_MAX) {
-        printf("bad --shape: D=%d exceeds ATTN_D_MAX=%d of this build\n", sd, ATTN_D_MAX);
-        return 2;
-    }
-    if (g_warmup < 0)
-        g_warmup = 0;
-    if (g_iters < 0)
-        g_iters = 0;
-    if (g_bench_secs <= 0)
-        g_bench_secs = 0.5;
-    if (pickcheck)
-        return check_pick_bk() ? 0 : 1;
+    struct shape custom;
+    if (cfg.shape_text && !parse_shape(cfg.shape_text, &custom))
+        return EXIT_BAD_USAGE;
+    if (cfg.warmup < 0)
+        cfg.warmup = 0;
+    if (cfg.iters < 0)
+        cfg.iters = 0;
+    if (!(cfg.min_secs > 0.0))
+        cfg.min_secs = 0.5;
+    if (cfg.pick_selftest)
+        return pick_selftest() ? EXIT_ALL_PASS : EXIT_CASE_FAILED;
 
     int ndev = 0;
     if (attn_dev_count(&ndev) != 0 || ndev < 1) {
-        printf("no HIP device visible: this harness runs on an MI355X\n");
-        return 1;
+        printf("flash_cli: no HIP device is visible; run this on the GPU\n");
+        return EXIT_CASE_FAILED;
     }
-    if (g_llc_bytes == 0)
-        g_llc_bytes = detect_llc_bytes();
-    char name[128] = "", arch[64] = "";
-    int cus = 0, clk = 0, l2 = 0;
-    attn_dev_info(name, sizeof name, arch, sizeof arch, &cus, &clk, &l2);
-    printf("=== FLASH bf16 attention (online softmax, gfx950 MFMA vs fp32 ref) ===\n");
-    printf("device: %s (%s), %d CUs, %d MHz, L2 %d KiB\n", name, arch, cus, clk / 1000, l2 / 1024);
-    printf("bk=%d (RUNTIME, --bk N to change; scratch %zu B at D=128); V-pack: %s\n", bk,
-           attn_flash_scratch_bytes(128, bk),
-           prepack_v ? "SEPARATE operator (v_prepacked=1)" : "inside kernel (LDS transposed reads)");
-    printf("per-phase times pv/qk/sm/sv = packv / qxk / softmax / sxv, seconds (one fused kernel: "
-           "all of it in qk)\n");
-    {
-        char tdesc[64];
-        if (g_iters > 0)
-            snprintf(tdesc, sizeof tdesc, "%d timed runs/case", g_iters);
-        else
-            snprintf(tdesc, sizeof tdesc, "adaptive >=%.2gs/case (min %d)", g_bench_secs,
-                     BENCH_MIN_REPS);
-        printf("timing: %d warmup + %s, mean device time per call (HIP events); HBM-cold input "
-               "pool >= %ux LLC=%.1f MiB (per line: /it = mean seconds, xN = runs, hbm Cx=MiB = "
-               "pool)\n",
-               g_warmup, tdesc, BENCH_DDR_MULT, (double)g_llc_bytes / (1024.0 * 1024.0));
+    if (cfg.llc_mib > 0) {
+        g_cache_bytes = (size_t)cfg.llc_mib << 20;
+    } else {
+        int l2 = 0;
+        if (attn_dev_info(NULL, 0, NULL, 0, NULL, NULL, &l2) != 0 || l2 < 0)
+            l2 = 0;
+        g_cache_bytes = (size_t)l2 + MI355X_INFINITY_CACHE;
     }
-    if (sweep) {
-        int ok = have_shape ? sweep_bk(shq, shkv, ssq, ssk, sd, scausal, srefcap, prepack_v)
-                            : sweep_bk(4, 2, 128, 1024, 128, 0, 0, prepack_v);
-        printf("=== %s ===\n", ok ? "ALL PASS" : "SOME FAILED");
-        return ok ? 0 : 1;
-    }
-    if (have_shape) {
-        int ok = run_case("custom shape", shq, shkv, ssq, ssk, sd, scausal, srefcap, bk, prepack_v);
-        printf("=== %s ===\n", ok ? "ALL PASS" : "SOME FAILED");
-        return ok ? 0 : 1;
-    }
+    print_banner();
+
     int all = 1;
-    all &= run_case("MHA prefill", 4, 4, 8, 8, 64, 0, 0, bk, prepack_v);
-    all &= run_case("MHA prefil.causal", 4, 4, 8, 8, 64, 1, 0, bk, prepack_v);
-    all &= run_case("GQA prefill", 8, 2, 8, 8, 64, 0, 0, bk, prepack_v);
-    all &= run_case("GQA prefil.causal", 8, 2, 8, 8, 64, 1, 0, bk, prepack_v);
-    all &= run_case("MHA decode(Sq=1)", 4, 4, 1, 16, 64, 0, 0, bk, prepack_v);
-    all &= run_case("GQA decode(Sq=1)", 8, 2, 1, 16, 64, 0, 0, bk, prepack_v);
-    all &= run_case("MQA prefill", 8, 1, 8, 8, 64, 0, 0, bk, prepack_v);
-    all &= run_case("odd + multiblock", 6, 3, 130, 70, 40, 1, 0, bk, prepack_v);
-    all &= run_case("GQA big head_dim", 8, 2, 4, 12, 128, 0, 0, bk, prepack_v);
-    if (longrun) {
-        printf("--- Qwen3 prefill sweep: Hq=16 Hkv=8 (GQA group=2) D=128 causal ---\n");
-        printf("  GFLOP = causal-correct USEFUL flops = 4*Hq*D*#{(i,j): j<=i}\n");
-        printf("  [ref:N rows spread 0..Sq-1]: the fp32 ref checks N rows spread over the whole\n");
-        printf("  sequence, including row Sq-1, which attends every key block.\n");
-        all &= run_case("qwen3 1k", 16, 8, 1024, 1024, 128, 1, 8, bk, prepack_v);
-        all &= run_case("qwen3 2k", 16, 8, 2048, 2048, 128, 1, 8, bk, prepack_v);
-        all &= run_case("qwen3 4k", 16, 8, 4096, 4096, 128, 1, 8, bk, prepack_v);
-    } else
-        printf("(default = 9 short shapes; --shape Hq,Hkv,Sq,Sk,D[,causal]: one custom case,\n"
-               " e.g. --shape 16,8,1024,1024,128,1 for qwen3 1k; --long: Qwen3 1k/2k/4k sweep;\n"
-               " --bk/--prepack-v/--iters/--warmup/--bench-secs/--llc-mb: tune the benchmark)\n");
+    if (cfg.sweep) {
+        static const struct shape sweep_default = {"sweep", 4, 2, 128, 1024, 128, 0, 0};
+        all = sweep_bk(cfg.shape_text ? &custom : &sweep_default);
+    } else if (cfg.shape_text) {
+        all = run_one(&custom);
+    } else {
+        for (int i = 0; i < COUNT(suite); i++)
+            all = run_one(&suite[i]) && all;
+        if (cfg.suite_long) {
+            printf("--- causal Qwen3 prefill: 16 query heads on 8 kv heads (g2), D=128; GFLOP "
+                   "counts useful (unmasked) pairs only; each case checks 8 rows spread over "
+                   "0..Sq-1, the last of which sees every key ---\n");
+            for (int i = 0; i < COUNT(qwen3_sweep); i++)
+                all = run_one(&qwen3_sweep[i]) && all;
+        } else {
+            printf("(--long adds the causal Qwen3 1k/2k/4k prefill; --shape runs one case of "
+                   "your own; --help lists every option)\n");
+        }
+    }
     printf("=== %s ===\n", all ? "ALL PASS" : "SOME FAILED");
-    return all ? 0 : 1;
+    return all ? EXIT_ALL_PASS : EXIT_CASE_FAILED;
 }

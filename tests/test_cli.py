@@ -1,5 +1,6 @@
-"""The command-line harness (tests/harness/flash_cli): the reference's `flash` program's
-flags, verdict lines and exit codes (flash.c:1177-1321), run against libattn_flash.so.
+"""The command-line harness (tests/harness/flash_cli): the option names, verdict lines and exit
+codes of the reference's `flash` program (flash.c:1151-1156,1177-1321), run against
+libattn_flash.so.
 
 CPU tests cover everything that ends before the first device call: argument errors (exit 2),
 the refused --no-softmax, and the attn_flash_pick_bk self-test. GPU tests run the default
@@ -35,15 +36,22 @@ def run(cli, *args, timeout=300):
 
 # ---- host-only paths -------------------------------------------------------------------------
 @pytest.mark.parametrize("args,needle", [
-    (["--bk", "48"], "bad --bk 48"),
-    (["--bk", "8"], "bad --bk 8"),
-    (["--bk", "8192"], "bad --bk 8192"),
-    (["--shape", "3,2,8,8,64"], "bad --shape"),
-    (["--shape", "4,4,0,8,64"], "bad --shape"),
-    (["--shape", "4,4"], "bad --shape: need Hq,Hkv,Sq,Sk,D"),
-    (["--shape", "4,4,8,8,257"], "exceeds ATTN_D_MAX"),
-    (["--frobnicate"], "unknown argument: --frobnicate"),
-    (["--no-softmax"], "--no-softmax: not available"),
+    (["--bk", "48"], "--bk 48 rejected"),
+    (["--bk", "8"], "--bk 8 rejected"),
+    (["--bk", "8192"], "--bk 8192 rejected"),
+    (["--bk", "x"], "wants an integer"),
+    (["--bk"], "needs a value"),
+    (["--shape", "3,2,8,8,64"], "Hq a multiple of Hkv"),
+    (["--shape", "4,4,0,8,64"], "must be positive"),
+    (["--shape", "4,4"], "wants 5 to 7 comma-separated integers"),
+    (["--shape", "4,4,8,8,64,"], "wants 5 to 7 comma-separated integers"),
+    (["--shape", "4,4,8,8,64,1,8,9"], "wants 5 to 7 comma-separated integers"),
+    (["--shape", "4,4,8,8,257"], "above ATTN_D_MAX=256"),
+    (["--shape", "4,4,8,8,64,1,-1"], "ref_cap must be >= 0"),
+    (["--iters", "3.5"], "wants an integer"),
+    (["--bench-secs", "fast"], "wants a number"),
+    (["--frobnicate"], "unrecognised option '--frobnicate'"),
+    (["--no-softmax"], "--no-softmax is rejected"),
 ])
 def test_bad_arguments_exit_2(cli, args, needle):
     r = run(cli, *args)
@@ -108,4 +116,5 @@ def test_sweep_bk(cli):
     rows = [l.split() for l in r.stdout.splitlines() if re.match(r"^\s+\d+\s+\d+\s", l)]
     assert [int(x[0]) for x in rows] == [16 << i for i in range(9)]
     assert all(x[-1] == "PASS" for x in rows)
-    assert "fastest bk=" in r.stdout and "attn_flash_pick_bk(D=128" in r.stdout
+    assert "every bk runs the same kernel" in r.stdout
+    assert "spread over bk:" in r.stdout and "attn_flash_pick_bk(D=128" in r.stdout
