@@ -90,7 +90,7 @@ def test_scratch_bytes_contract():
         assert all(s % ts.ATTN_SCRATCH_ALIGN == 0 for s in sizes)
         assert sizes == sorted(sizes)  # monotone non-decreasing in bk
     assert ts.attn_flash_scratch_bytes(128, 128) >= ts.attn_flash_scratch_bytes(64, 128)
-    # capacity: 32768 split slots of (m, l, acc[D]) fp32
+    # capacity: 65536 split slots of (m, l, acc[D]) fp32
     assert ts.attn_flash_scratch_bytes(128, 128) >= 65536 * (128 + 2) * 4
 
 
