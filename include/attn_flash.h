@@ -76,6 +76,21 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
  * pack_v_full). Device pointers, stream-ordered like attn_flash. */
 void pack_v_full(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D);
 
+/* Allocation-free variant of attn_flash. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory or own a scratch (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and semantics as attn_flash,
+ * without scratch and tm; the split-K partials go to a static device array of
+ * ATTN_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on until the process
+ * ends (the layout of attn_flash's scratch at D = ATTN_NOALLOC_D_MAX, so the kernels, the splits
+ * and the output are those of attn_flash). It calls no hipMalloc, hipFree or other allocating
+ * routine. D above ATTN_NOALLOC_D_MAX is rejected (stderr message, then abort), as is everything
+ * attn_flash rejects. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the caller. */
+#define ATTN_NOALLOC_D_MAX 128
+#define ATTN_NOALLOC_SCRATCH_BYTES 34078720u /* = attn_flash_scratch_bytes(128, any bk) */
+void attn_flash_noalloc(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O, int Hq,
+                        int Hkv, int Sq, int Sk, int D, int causal, int bk, int v_prepacked);
+
 /* Stream selection for the calling thread (no counterpart in the reference, which has
  * no device). `stream` is a hipStream_t; NULL selects the null stream. */
 void attn_flash_set_stream(void *stream);

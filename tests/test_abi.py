@@ -128,6 +128,33 @@ def test_bad_shapes_abort(args, msg):
     assert msg in r.stderr
 
 
+def test_noalloc_static_scratch_size():
+    """The static array of attn_flash_noalloc is the layout of attn_flash's scratch at its largest
+    D, so every D it accepts carves the same slots as a caller's scratch would."""
+    text = open(os.path.join(ROOT, "include", "attn_flash.h")).read()
+    m = re.search(r"#define ATTN_NOALLOC_SCRATCH_BYTES (\d+)u", text)
+    assert m and int(m.group(1)) == ts.ATTN_NOALLOC_SCRATCH_BYTES
+    assert re.search(r"#define ATTN_NOALLOC_D_MAX %d\b" % ts.ATTN_NOALLOC_D_MAX, text)
+    for bk in (16, 128, 4096):
+        assert ts.attn_flash_scratch_bytes(ts.ATTN_NOALLOC_D_MAX, bk) == \
+            ts.ATTN_NOALLOC_SCRATCH_BYTES
+    assert all(ts.attn_flash_scratch_bytes(d, 128) <= ts.ATTN_NOALLOC_SCRATCH_BYTES
+               for d in range(1, ts.ATTN_NOALLOC_D_MAX + 1))
+
+
+@pytest.mark.parametrize("args,msg", [
+    ("1, 2, 3, 4, 4, 4, 8, 8, 129, 0, 128", "D=129 is invalid -- the static scratch holds"),
+    ("1, 2, 3, 4, 4, 4, 8, 8, 256, 0, 128", "D=256 is invalid -- the static scratch holds"),
+    ("1, 2, 3, 4, 4, 4, 8, 8, 64, 0, 100", "attn_flash_noalloc: bk=100 is invalid"),
+    ("1, 2, 3, 4, 6, 4, 8, 8, 64, 0, 128", "Hq % Hkv"),
+    ("0, 2, 3, 4, 4, 4, 8, 8, 64, 0, 128", "device pointers"),
+])
+def test_noalloc_rejects_before_any_device_call(args, msg):
+    r = _run_py("import transfer_station_amd as ts; ts.attn_flash_noalloc(%s)" % args)
+    assert r.returncode == -signal.SIGABRT
+    assert msg in r.stderr
+
+
 def test_bad_d_aborts_in_size_query():
     r = _run_py("import transfer_station_amd as ts; ts.attn_flash_scratch_bytes(0, 128)")
     assert r.returncode == -signal.SIGABRT and "D=0 is invalid" in r.stderr

@@ -17,6 +17,8 @@ ATTN_BK_MAX = 4096
 ATTN_BK_DEFAULT = 128
 ATTN_SCRATCH_ALIGN = 64
 ATTN_D_MAX = 256
+ATTN_NOALLOC_D_MAX = 128
+ATTN_NOALLOC_SCRATCH_BYTES = 34078720
 
 
 class AttnTimes(ctypes.Structure):
@@ -98,6 +100,14 @@ def attn_flash(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, bk, scratch, v_prepacked=
     lib().attn_flash(_addr(Q), _addr(K), _addr(V), _addr(O), int(Hq), int(Hkv), int(Sq),
                      int(Sk), int(D), int(bool(causal)), int(bk), _addr(scratch),
                      int(v_prepacked), ctypes.byref(tm) if tm is not None else None)
+
+
+def attn_flash_noalloc(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=0):
+    """attn_flash without a scratch argument: the split-K partials go to the library's static
+    device array (no allocation). D above ATTN_NOALLOC_D_MAX aborts. Calls that overlap on one
+    GPU race on that array."""
+    lib().attn_flash_noalloc(_addr(Q), _addr(K), _addr(V), _addr(O), int(Hq), int(Hkv), int(Sq),
+                             int(Sk), int(D), int(bool(causal)), int(bk), int(v_prepacked))
 
 
 def pack_v_full(V, Vp, Hkv, Sk, D):

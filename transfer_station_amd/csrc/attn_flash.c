@@ -28,6 +28,7 @@ int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, f
                           int D, int nsplit, float c, int Sq, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
 int attn_hip_device_cus(void);
+int attn_hip_static_scratch(void **ptr, size_t *bytes);
 
 /* ---- device scratch layout ---------------------------------------------------------------
  * Split-K partial slots, one per (query row, split): m[ATTN_SLOTS], l[ATTN_SLOTS] and
@@ -176,14 +177,14 @@ static void attn_events(void) {
         attn_hip_check(hipEventCreate(&t_ev1), "attn_flash(tm)");
 }
 
-void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O, int Hq,
-                int Hkv, int Sq, int Sk, int D, int causal, int bk, void *scratch,
-                int v_prepacked, struct attn_times *tm) {
-    static const char *who = "attn_flash";
-    /* bk keeps the reference's contract (validated here, scratch sized with it), but the key
-     * tile is the hardware's: 128 keys up to D = 128, 64 beyond, whatever bk says. In the
-     * reference bk is a cache-blocking knob whose result is bk-invariant within the tolerance
-     * (README.md:354-357); on the GPU a smaller tile is only slower. */
+/* Argument checks shared by both attention entry points. bk keeps the reference's contract
+ * (validated here, scratch sized with it), but the key tile is the hardware's: 128 keys up to
+ * D = 128, 64 beyond, whatever bk says. In the reference bk is a cache-blocking knob whose
+ * result is bk-invariant within the tolerance (README.md:354-357); on the GPU a smaller tile is
+ * only slower. */
+static void attn_check_args(const char *who, const uint16_t *Q, const uint16_t *K,
+                            const uint16_t *V, const float *O, int Hq, int Hkv, int Sq, int Sk,
+                            int D, int bk) {
     attn_bk_check(bk, who);
     attn_d_check(D, who);
     if (Hkv < 1 || Hq < 1 || Hq % Hkv != 0)
@@ -192,9 +193,13 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         attn_fail(who, "need Sq >= 1 and Sk >= 1");
     if (!Q || !K || !V || !O)
         attn_fail(who, "Q, K, V and O must be device pointers");
-    if (!scratch || ((uintptr_t)scratch % ATTN_SCRATCH_ALIGN) != 0)
-        attn_fail(who, "scratch must be non-NULL and ATTN_SCRATCH_ALIGN-aligned");
+}
 
+/* Kernel choice and launches on the calling thread's stream; `scratch` holds the split-K
+ * partial slots (attn_layout at this D). */
+static void attn_run(const char *who, const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                     float *O, int Hq, int Hkv, int Sq, int Sk, int D, int causal, void *scratch,
+                     int v_prepacked, struct attn_times *tm) {
     void *st = t_stream;
     const int group = Hq / Hkv;
     const float scale = 1.0f / sqrtf((float)D);
@@ -238,6 +243,38 @@ void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *
         attn_hip_check(hipEventElapsedTime(&ms, t_ev0, t_ev1), who);
         tm->qxk += (double)ms * 1e-3;
     }
+}
+
+void attn_flash(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O, int Hq,
+                int Hkv, int Sq, int Sk, int D, int causal, int bk, void *scratch,
+                int v_prepacked, struct attn_times *tm) {
+    static const char *who = "attn_flash";
+    attn_check_args(who, Q, K, V, O, Hq, Hkv, Sq, Sk, D, bk);
+    if (!scratch || ((uintptr_t)scratch % ATTN_SCRATCH_ALIGN) != 0)
+        attn_fail(who, "scratch must be non-NULL and ATTN_SCRATCH_ALIGN-aligned");
+    attn_run(who, Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, scratch, v_prepacked, tm);
+}
+
+/* No hipMalloc and no events: the partial slots are the library's static device array, whose
+ * address is resolved once per device (attn_hip_static_scratch). */
+void attn_flash_noalloc(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                        int Hq, int Hkv, int Sq, int Sk, int D, int causal, int bk,
+                        int v_prepacked) {
+    static const char *who = "attn_flash_noalloc";
+    attn_check_args(who, Q, K, V, O, Hq, Hkv, Sq, Sk, D, bk);
+    if (D > ATTN_NOALLOC_D_MAX) {
+        fprintf(stderr,
+                "%s: D=%d is invalid -- the static scratch holds partials for D <= %d "
+                "(use attn_flash with a caller-owned scratch)\n",
+                who, D, ATTN_NOALLOC_D_MAX);
+        abort();
+    }
+    void *scratch = NULL;
+    size_t bytes = 0;
+    attn_hip_check(attn_hip_static_scratch(&scratch, &bytes), who);
+    if (bytes < attn_layout(NULL, D, NULL) || ((uintptr_t)scratch % ATTN_SCRATCH_ALIGN) != 0)
+        attn_fail(who, "static scratch is smaller than its layout or misaligned");
+    attn_run(who, Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, scratch, v_prepacked, NULL);
 }
 
 void pack_v_full(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D) {

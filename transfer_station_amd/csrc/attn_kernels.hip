@@ -24,7 +24,10 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <type_traits>
+
+#include "attn_flash.h"
 
 namespace {
 
@@ -1427,5 +1430,42 @@ extern "C" int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, 
         if (e != hipSuccess)
             return (int)e;
     }
+    return (int)hipSuccess;
+}
+
+// ---- allocation-free scratch (attn_flash_noalloc) -------------------------------------------
+// The split-K partial slots of attn_flash_noalloc: the layout of a caller's attn_flash scratch
+// at D = ATTN_NOALLOC_D_MAX, one copy per GPU, held until the process ends. The kernels write
+// every slot they later read, so nothing in it has to start at zero. In host code the name
+// `scratch` is a host-side stand-in, not a device address: the device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only that address is
+// ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_addr[kMaxDevices]; // per device; zero until first resolved
+} // namespace
+
+// Device address and size of the current device's static scratch. Two threads that resolve it
+// at once both store the same address, so no lock is needed.
+extern "C" int attn_hip_static_scratch(void **ptr, size_t *bytes) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return (int)e;
+    if (dev < 0 || dev >= kMaxDevices)
+        return (int)hipErrorInvalidDevice;
+    void *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess)
+            return (int)e;
+        if (!p)
+            return (int)hipErrorInvalidSymbol;
+        g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+    *ptr = p;
+    *bytes = sizeof(scratch);
     return (int)hipSuccess;
 }
