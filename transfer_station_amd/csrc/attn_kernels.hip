@@ -565,9 +565,10 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
         vto[k] = (uint32_t)e * (uint32_t)Sk * 2u + (uint32_t)kc * 16u;
         vtk[k] = (e < D) ? kc * 8 : 0x7fffffff; // d rows past D: never in range
     }
-    auto dma_tile = [&](int kt, int buf) {
-        // Row-major K and V: descriptors based at the tile (scalar work), whose range still ends
-        // at the head's last byte, so the per-lane offsets stay loop-invariant.
+    // K (or V) tile kt into LDS buffer buf. Row-major K and V: descriptors based at the tile
+    // (scalar work), whose range still ends at the head's last byte, so the per-lane offsets stay
+    // loop-invariant.
+    auto dma_k = [&](int kt, int buf) {
         const uint32_t toff = (uint32_t)kt * KT * D * 2;
         const __amdgpu_buffer_rsrc_t rkt = make_rsrc(K + (size_t)u * Sk * D + (size_t)kt * KT * D,
                                                      kvbytes - toff);
@@ -575,6 +576,8 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
         for (int k = 0; k < PW; ++k)
             if (NI % NW == 0 || k < nblk_w)
                 dma16<0>(rkt, &Ks[buf][(w * PW + k) * 512], kso[k]);
+    };
+    auto dma_v = [&](int kt, int buf) {
         if constexpr (VT) {
             const int klim = Sk - kt * KT; // keys of this tile that exist
 #pragma unroll
@@ -583,6 +586,7 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
                     dma16<0>(rv, &Vs[buf][(w * PW + k) * 512],
                              vtk[k] < klim ? vto[k] + (uint32_t)kt * KT * 2 : 0x80000000u);
         } else {
+            const uint32_t toff = (uint32_t)kt * KT * D * 2;
             const __amdgpu_buffer_rsrc_t rvt =
                 make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D, kvbytes - toff);
 #pragma unroll
@@ -608,126 +612,156 @@ __global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_f
                        : hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
                              (i16 & 1) * 4;
 
-    if (kt0 < kt1)
-        dma_tile(kt0, 0);
-    // Q and this wave's DMA blocks of the first tile have landed. Q must be resident before
-    // the loop: otherwise the compiler's wait at the loop's first MFMA also waits for the next
-    // tile's prefetch (its count cannot tell the two apart). 0x0F70 = vmcnt(0), expcnt and
-    // lgkmcnt unconstrained (gfx9 encoding).
+    f32x16 s[KT / 32];
+    bf16x8 pk[KT / 16];
+    // S^T = K_tile . Q^T for one key tile (LDS buffer buf) into s; the next 32-key sub-tile's K
+    // fragments are read between this sub-tile's MFMAs.
+    auto qk = [&](int buf) {
+        const uint16_t *kb0 = &Ks[buf][kfo];
+        bf16x8 ka[2][DP / 16];
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+            ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
+        __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                s[t][i] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < DP / 16; ++kk) {
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
+                if (t + 1 < KT / 32)
+                    ka[(t + 1) & 1][kk] = as_bf16x8(
+                        *reinterpret_cast<const u32x4 *>(kb0 + (t + 1) * KSUB + kk * KDK));
+            }
+#pragma unroll
+            for (int kk = 0; kk < DP / 16; ++kk) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (t + 1 < KT / 32)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+    };
+    // Online softmax of the tile at key kbase: mask, row max, lazy rescale of (l, o), then
+    // p = 2^(s c - m c) into P (bf16, the B operand of P.V) and l += sum of the fp32 p.
+    auto softmax = [&](int kbase) {
+        if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin)) {
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kbase + t * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
+                    if (key > lim)
+                        s[t][i] = kNegInf;
+                }
+        }
+        // Row max: one max3 chain per 32-key sub-tile (two new scores per instruction), the
+        // chains combined, the partner half-row through the VALU exchange, then the
+        // wave-uniform lazy-rescale test.
+        float mt[KT / 32];
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t) {
+            float m = max3f(s[t][0], s[t][1], s[t][2]);
+#pragma unroll
+            for (int i = 3; i < 15; i += 2)
+                m = max3f(m, s[t][i], s[t][i + 1]);
+            mt[t] = fmaxf(m, s[t][15]);
+        }
+        float mx = mt[0];
+#pragma unroll
+        for (int j = 1; j < KT / 32; j += 2)
+            mx = (j + 1 < KT / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
+        mx = max_xor32(mx);
+        const bool raise = mx > m_run + lazy_raw;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+            const float mnew = raise ? mx : m_run;
+            const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+                o[db] *= alpha;
+            m_run = mnew;
+        }
+        const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
+        float ps[KT / 16];
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float p[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    p[j] = fast_exp2(fmaf(s[t][8 * hh + j], c, -mc));
+                    pk[2 * t + hh][j] = (__bf16)p[j];
+                }
+                ps[2 * t + hh] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < KT / 16; ++j)
+            psum += ps[j];
+        l_run += psum;
+    };
+    // O^T += V^T . P^T for the tile in LDS buffer buf. The V^T operand of 16-key chunk cc, d
+    // block db: one 16-byte read (V^T tile) or two transposed 8-byte reads (row-major V tile).
+    // Fragments are double-buffered a chunk ahead, so each read has the previous chunk's MFMAs
+    // to land in; chunk 0 is read by pv_first before the softmax, under its exponentials.
+    bf16x8 va[2][DP / 32];
+    auto vfrag = [&](int buf, int cc, int db) -> bf16x8 {
+        if (VT)
+            return as_bf16x8(
+                *reinterpret_cast<const u32x4 *>(&Vs[buf][vfo + cc * 128 + db * 32 * KT]));
+        const uint16_t *vb = &Vs[buf][vfo + cc * 16 * DP + db * 128];
+        return join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * DP));
+    };
+    auto pv_first = [&](int buf) {
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+            va[0][db] = vfrag(buf, 0, db);
+    };
+    auto pv = [&](int buf) {
+#pragma unroll
+        for (int cc = 0; cc < KT / 16; ++cc) {
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], o[db], 0, 0,
+                                                               0);
+                if (cc + 1 < KT / 16)
+                    va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
+            }
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (cc + 1 < KT / 16)
+                    __builtin_amdgcn_sched_group_barrier(0x100, VT ? 1 : 2, 0);
+            }
+        }
+    };
+
+    if (kt0 < kt1) {
+        dma_k(kt0, 0);
+        dma_v(kt0, 0);
+    }
+    // Q and this wave's DMA blocks of the first tile have landed. Q must be resident before the
+    // loop: otherwise the compiler's wait at the loop's first MFMA also waits for the next tile's
+    // prefetch (its count cannot tell the two apart). 0x0F70 = vmcnt(0), expcnt and lgkmcnt
+    // unconstrained (gfx9 encoding).
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     for (int kt = kt0; kt < kt1; ++kt) {
         const int buf = (kt - kt0) & 1;
         // The other buffer's last readers finished before the barrier that ended tile kt-1.
-        if (kt + 1 < kt1)
-            dma_tile(kt + 1, buf ^ 1);
+        if (kt + 1 < kt1) {
+            dma_k(kt + 1, buf ^ 1);
+            dma_v(kt + 1, buf ^ 1);
+        }
         const int kbase = kt * KT;
         if (kbase <= wave_maxkey) {
-            f32x16 s[KT / 32];
-            const uint16_t *kb0 = &Ks[buf][kfo];
-            bf16x8 ka[2][DP / 16];
-#pragma unroll
-            for (int kk = 0; kk < DP / 16; ++kk)
-                ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
-            __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
-#pragma unroll
-            for (int t = 0; t < KT / 32; ++t) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    s[t][i] = 0.f;
-                // The next sub-tile's K fragments are read between this sub-tile's MFMAs.
-#pragma unroll
-                for (int kk = 0; kk < DP / 16; ++kk) {
-                    s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
-                    if (t + 1 < KT / 32)
-                        ka[(t + 1) & 1][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
-                            kb0 + (t + 1) * KSUB + kk * KDK));
-                }
-#pragma unroll
-                for (int kk = 0; kk < DP / 16; ++kk) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (t + 1 < KT / 32)
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-            }
-            if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin)) {
-#pragma unroll
-                for (int t = 0; t < KT / 32; ++t)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key = kbase + t * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
-                        if (key > lim)
-                            s[t][i] = kNegInf;
-                    }
-            }
-            // Row max of the tile: one max3 chain per 32-key sub-tile (two new scores per
-            // instruction), the chains combined, the partner half-row through the VALU exchange,
-            // then the wave-uniform lazy-rescale test; the exponentials and the P.V MFMAs follow
-            // in one branch-free block.
-            float mt[KT / 32];
-#pragma unroll
-            for (int t = 0; t < KT / 32; ++t) {
-                float m = max3f(s[t][0], s[t][1], s[t][2]);
-#pragma unroll
-                for (int i = 3; i < 15; i += 2)
-                    m = max3f(m, s[t][i], s[t][i + 1]);
-                mt[t] = fmaxf(m, s[t][15]);
-            }
-            float mx = mt[0];
-#pragma unroll
-            for (int j = 1; j < KT / 32; j += 2)
-                mx = (j + 1 < KT / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
-            mx = max_xor32(mx);
-            const bool raise = mx > m_run + lazy_raw;
-            if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-                const float mnew = raise ? mx : m_run;
-                const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < DP / 32; ++db)
-                    o[db] *= alpha;
-                m_run = mnew;
-            }
-            const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
-            bf16x8 pk[KT / 16];
-            float ps[KT / 16];
-#pragma unroll
-            for (int t = 0; t < KT / 32; ++t)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float p[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        p[j] = fast_exp2(fmaf(s[t][8 * hh + j], c, -mc));
-                        pk[2 * t + hh][j] = (__bf16)p[j];
-                    }
-                    ps[2 * t + hh] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-                }
-            float psum = 0.f;
-#pragma unroll
-            for (int j = 0; j < KT / 16; ++j)
-                psum += ps[j];
-            l_run += psum;
-#pragma unroll
-            for (int cc = 0; cc < KT / 16; ++cc) {
-                if (VT) {
-                    const uint16_t *vb = &Vs[buf][vfo + cc * 128];
-#pragma unroll
-                    for (int db = 0; db < DP / 32; ++db) {
-                        const bf16x8 a =
-                            as_bf16x8(*reinterpret_cast<const u32x4 *>(vb + db * 32 * KT));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
-                    }
-                } else {
-                    const uint16_t *vb = &Vs[buf][vfo + cc * 16 * DP];
-#pragma unroll
-                    for (int db = 0; db < DP / 32; ++db) {
-                        const bf16x8 a = join_tr(lds_read_tr(vb + db * 128),
-                                                 lds_read_tr(vb + db * 128 + 4 * DP));
-                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db], 0, 0, 0);
-                    }
-                }
-            }
+            qk(buf);
+            pv_first(buf);
+            softmax(kbase);
+            pv(buf);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
         __syncthreads();
