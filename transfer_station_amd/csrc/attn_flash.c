@@ -14,6 +14,7 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 /* HIP launchers (attn_kernels.hip). Each returns a hipError_t. */
 int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
@@ -136,7 +137,16 @@ void *attn_flash_get_stream(void) { return t_stream; }
  * the prefill's MFMA tiles win. Measured, Sk = 4096, 32-64 rows per kv head: 512 kv heads
  * prefill 1.4-2.1x faster; 32-64 kv heads decode 1.7-2x faster. */
 static int attn_use_decode(int Hkv, int group, int Sq) {
+    /* ATTN_PATH=decode or =prefill (read once) forces the kernel for tuning sweeps, decode only
+     * where its row blocks apply (g*Sq <= 64). */
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("ATTN_PATH");
+        forced = (e && !strcmp(e, "decode")) ? 1 : ((e && !strcmp(e, "prefill")) ? 2 : 0);
+    }
     const long rows = (long)group * Sq;
+    if (forced == 2 || (forced == 1 && rows <= ATTN_DECODE_MAX_ROWS))
+        return forced == 1;
     if (rows <= ATTN_DECODE_ROWS)
         return 1;
     return rows <= ATTN_DECODE_MAX_ROWS && Hkv < attn_hip_device_cus();
@@ -219,7 +229,7 @@ static void attn_run(const char *who, const uint16_t *Q, const uint16_t *K, cons
         const int nrb = (group * Sq + ATTN_DECODE_ROWS - 1) / ATTN_DECODE_ROWS;
         int nsplit, kps;
         attn_decode_split(Hq, Hkv, Sq, Sk, nrb, &nsplit, &kps);
-        struct attn_carve cv;
+        struct attn_carve cv = {NULL, NULL, NULL};
         attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_decode(Q, K, V, O, cv.m, cv.l, cv.acc, Hq, Hkv, Sq, Sk, D,
                                               causal ? 1 : 0, vec, vt, dp, c, nsplit, kps, nrb,
@@ -229,7 +239,7 @@ static void attn_run(const char *who, const uint16_t *Q, const uint16_t *K, cons
             attn_hip_check(
                 attn_hip_launch_merge(cv.m, cv.l, cv.acc, O, Hq * Sq, D, nsplit, c, Sq, st), who);
     } else {
-        struct attn_carve cv;
+        struct attn_carve cv = {NULL, NULL, NULL};
         attn_layout(scratch, D, &cv);
         attn_hip_check(attn_hip_launch_prefill(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal ? 1 : 0,
                                                vec, vt, dp, c, cv.m, cv.l, cv.acc, ATTN_SLOTS,

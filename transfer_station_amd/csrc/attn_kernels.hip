@@ -402,8 +402,14 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, u
                                              voff, 0, IMM, 0);
 }
 
+// Workgroups per CU the launch bounds ask for: 8 waves in all, unless the two K and V tiles
+// (8*KT*DP bytes of LDS) or the O and Q registers (DP > 128) allow only one workgroup.
+constexpr int prefill_wg_per_cu(int DP, int KT, int NW) {
+    return (DP > 128 || 8 * KT * DP > 80 * 1024) ? 1 : 8 / NW;
+}
+
 template <int DP, int KT, int NW, bool CAUSAL, bool VT>
-__global__ __launch_bounds__(NW * 64, DP > 128 ? 1 : 8 / NW) void attn_prefill_fast_kernel(
+__global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
@@ -1301,12 +1307,34 @@ static int prefill_waves(int Hq, int Hkv, int Sq, bool causal) {
     return (full && n8 <= (causal ? device_cus() : device_cus() / 2)) ? 4 : 8;
 }
 
+// ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
+// on 8-wave workgroups, or 128 keys on 4-wave workgroups at D > 64 (one such workgroup per CU).
+static int prefill_kt_forced() {
+    static int forced = -1;
+    if (forced < 0) {
+        const char *e = getenv("ATTN_PREFILL_KT");
+        forced = (e && (atoi(e) == 64 || atoi(e) == 128)) ? atoi(e) : 0;
+    }
+    return forced;
+}
+
 template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
+    const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, CAUSAL) : 4;
+    // Tuning override of the key tile (the other of 64 / 128 keys), non-V^T only; the counter
+    // study that fixed the defaults runs through it.
+    if constexpr (DP <= 128 && KT == 128 && !VT) {
+        if (prefill_kt_forced() == 64 && nw == 8)
+            return launch_prefill_fast_nw<DP, 64, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
+                                                                 pm, pl, pacc, slots, st);
+        if (prefill_kt_forced() == 128 && nw == 4 && DP > 64)
+            return launch_prefill_fast_nw<DP, 128, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
+                                                                  c, pm, pl, pacc, slots, st);
+    }
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
-        if (prefill_waves(Hq, Hkv, Sq, CAUSAL) == 8)
+        if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
                                                                  pm, pl, pacc, slots, st);
     // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
