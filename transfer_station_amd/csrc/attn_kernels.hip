@@ -16,6 +16,7 @@
 //                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
+//   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T with the V^T tile staged in LDS
 //   attn_merge_kernel                      log-sum-exp merge of the decode partials
 //   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
 //                                          vector path / any shape)
@@ -1011,6 +1012,212 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
 }
 
+// Decode from V^T ([Hkv][D][Sk], D % 8 == 0, Sk % 8 == 0, 16-byte aligned tensors, DP <= 128):
+// attn_decode_kernel's workgroups, rows, S MFMAs and softmax, but the V^T operand is staged
+// through LDS. Per 128-key step the workgroup's V^T tile (DP d rows x 256 bytes) arrives by
+// LDS-DMA, each 1 KB block covering 4 d rows x 256 contiguous bytes, where loading the operand
+// layout straight from memory takes 16 d rows x 64 bytes per instruction (half lines). The 16
+// 16-byte chunks of a d row e sit at chunk slot c ^ (e % 16), so the 16 lanes of an operand
+// read (16 d rows, one key chunk) hit 16 distinct bank groups. The tile is double-buffered
+// with one barrier per step, and the next step's K fragments are loaded under this step's work.
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_decode_vt_kernel(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+    const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
+    float *__restrict__ pl, float *__restrict__ pacc, int Hq, int Hkv, int Sq, int Sk, int D,
+    float c, int nsplit, int kps, int nrb) {
+    static_assert(DP % 32 == 0 && DP <= 128, "tile shape");
+    constexpr int STEP = 128;            // keys per workgroup step: 4 waves x 32
+    constexpr int TILE = DP * STEP;      // elements of one V^T step tile
+    constexpr int NB = DP / 4, PWB = NB / 4; // 1 KB DMA blocks per tile, per wave
+    __shared__ __attribute__((aligned(1024))) uint16_t Vt[2][TILE];
+    __shared__ float red_m[4][16], red_l[4][16];
+    static_assert(4 * 16 * DP * 4 <= 2 * TILE * 2, "merge area must fit in the V^T tiles");
+
+    const int g = Hq / Hkv, M = g * Sq;
+    const int L = (nrb > 1) ? xcd_remap((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+    const int rb = L % nrb, us = L / nrb;
+    const int u = us / nsplit, sp = us % nsplit;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, grp = lane >> 4;
+    const int k0 = sp * kps, k1 = min(k0 + kps, Sk);
+    const int row0 = 16 * rb, Mb = min(16, M - row0);
+
+    const bool rvalid = row0 + r16 < M;
+    const int gi = rvalid ? (row0 + r16) / Sq : 0, qi = rvalid ? (row0 + r16) % Sq : 0;
+    const int h = u * g + gi;
+    const uint16_t *Kh = K + (size_t)u * Sk * D;
+
+    bf16x8 qb[DP / 32];
+#pragma unroll
+    for (int kk = 0; kk < DP / 32; ++kk)
+        qb[kk] = as_bf16x8(
+            load_row8<true>(Q + (size_t)h * Sq * D, (size_t)qi, kk * 32 + grp * 8, D, rvalid));
+    const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + qi) : Sk - 1;
+
+    float m_run = kNegInf, l_run = 0.f;
+    f32x4 o[DP / 16];
+#pragma unroll
+    for (int db = 0; db < DP / 16; ++db)
+        o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // This lane's DMA sources: block b = w*PWB + k holds d rows 4b .. 4b+3; lane slot p = lane%16
+    // of row e = 4b + lane/16 receives source chunk p ^ (e%16). A chunk of a d row past D or of
+    // keys at or past k1 gets an offset beyond the buffer's range and lands as zeros.
+    const __amdgpu_buffer_rsrc_t rvt = make_rsrc(V + (size_t)u * D * Sk, (uint32_t)D * Sk * 2);
+    uint32_t vsrc[PWB];
+    int vkey[PWB];
+#pragma unroll
+    for (int k = 0; k < PWB; ++k) {
+        const int e = 4 * (w * PWB + k) + (lane >> 4);
+        const int cs = (lane & 15) ^ (e & 15);
+        vsrc[k] = (uint32_t)e * (uint32_t)Sk * 2u + (uint32_t)cs * 16u;
+        vkey[k] = (e < D) ? cs * 8 : 0x7fffffff;
+    }
+    auto dma_step = [&](int step, int buf) {
+        const int key0 = k0 + step * STEP;
+        const int klim = k1 - key0; // keys of this step inside the split
+#pragma unroll
+        for (int k = 0; k < PWB; ++k)
+            dma16<0>(rvt, &Vt[buf][(w * PWB + k) * 512],
+                     vkey[k] < klim ? vsrc[k] + (uint32_t)key0 * 2u : 0x80000000u);
+    };
+    u32x4 ka[2][DP / 32], kn[2][DP / 32];
+    auto load_k = [&](int step, u32x4 (&dst)[2][DP / 32]) {
+        const int tb = k0 + step * STEP + w * 32;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
+#pragma unroll
+            for (int kk = 0; kk < DP / 32; ++kk)
+                dst[t][kk] = load_row8<true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+        }
+    };
+
+    // Each workgroup starts its walk over the steps at a different step (spreads the V^T rows,
+    // 2*Sk bytes apart, over more HBM channels; see attn_decode_kernel).
+    const int nsteps = (k1 - k0 + STEP - 1) / STEP;
+    const int rot = us % (nsteps > 0 ? nsteps : 1);
+    auto step_of = [&](int js) { return (js + rot < nsteps) ? js + rot : js + rot - nsteps; };
+    if (nsteps > 0) {
+        dma_step(step_of(0), 0);
+        load_k(step_of(0), ka);
+    }
+    for (int js = 0; js < nsteps; ++js) {
+        const int buf = js & 1;
+        // This step's tile and K fragments have landed in every wave; every wave is done with
+        // the other buffer (read in step js-1).
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (js + 1 < nsteps) {
+            dma_step(step_of(js + 1), buf ^ 1);
+            load_k(step_of(js + 1), kn);
+        }
+        const int tb = k0 + step_of(js) * STEP + w * 32;
+        if (tb < k1) {
+            f32x4 s[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < DP / 32; ++kk)
+                    s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][kk]), qb[kk],
+                                                                   s[t], 0, 0, 0);
+            }
+            // Register (t, i) of this lane holds key tb + 8grp + 4t + i for row r16.
+            float mx = kNegInf;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = tb + 8 * grp + 4 * t + i;
+                    if (key >= k1 || key > lim)
+                        s[t][i] = kNegInf;
+                    mx = fmaxf(mx, s[t][i]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(m_run, mx);
+            const float muse = (mnew == kNegInf) ? 0.f : mnew;
+            const float alpha = fast_exp2((m_run - muse) * c);
+            const float mc = muse * c;
+            float psum = 0.f;
+            bf16x8 pk;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = fast_exp2(fmaf(s[t][i], c, -mc));
+                    psum += p;
+                    pk[4 * t + i] = (__bf16)p;
+                }
+            l_run = alpha * l_run + psum;
+            m_run = mnew;
+            // V^T operand: d row 16db + r16, keys of chunk w*4 + grp (this wave's 32 keys).
+            const int cs = w * 4 + grp;
+#pragma unroll
+            for (int db = 0; db < DP / 16; ++db) {
+                o[db] *= alpha;
+                const int e = db * 16 + r16;
+                const bf16x8 a = as_bf16x8(
+                    *reinterpret_cast<const u32x4 *>(&Vt[buf][e * STEP + ((cs ^ (e & 15)) * 8)]));
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
+            }
+        }
+        if (js + 1 < nsteps) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int kk = 0; kk < DP / 32; ++kk)
+                    ka[t][kk] = kn[t][kk];
+        }
+    }
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+
+    // Merge the 4 waves (as attn_decode_kernel): O^T register (db, i) holds d = 16db + 4grp + i.
+    __syncthreads();
+    float *om = reinterpret_cast<float *>(&Vt[0][0]); // [4][16][DP]
+    if (grp == 0) {
+        red_m[w][r16] = m_run;
+        red_l[w][r16] = l_run;
+    }
+#pragma unroll
+    for (int db = 0; db < DP / 16; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            om[(w * 16 + r16) * DP + db * 16 + 4 * grp + i] = o[db][i];
+    __syncthreads();
+    for (int idx = tid; idx < Mb * D; idx += 256) {
+        const int r = idx / D, d = idx - r * D;
+        float mx = kNegInf;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww)
+            mx = fmaxf(mx, red_m[ww][r]);
+        const float muse = (mx == kNegInf) ? 0.f : mx;
+        float acc = 0.f, lsum = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+            const float wgt = fast_exp2((red_m[ww][r] - muse) * c);
+            acc += wgt * om[(ww * 16 + r) * DP + d];
+            lsum += wgt * red_l[ww][r];
+        }
+        const int hr = u * g + (row0 + r) / Sq, qr = (row0 + r) % Sq;
+        const size_t orow = (size_t)hr * Sq + qr;
+        if (nsplit == 1) {
+            O[orow * D + d] = acc * ((lsum > 0.f) ? 1.0f / lsum : 0.f);
+        } else {
+            const size_t slot = orow * nsplit + sp;
+            pacc[slot * D + d] = acc;
+            if (d == 0) {
+                pm[slot] = mx;
+                pl[slot] = lsum;
+            }
+        }
+    }
+}
+
 // Merge of split-K partials. Partial row r owns slots r*nsplit .. r*nsplit+nsplit-1 and covers
 // row q_off + r % rph of query head r / rph, so its O row is (r / rph) * Sq + q_off + r % rph
 // (decode: rph = Sq, q_off = 0). Weights w_s = 2^((m_s - max m) c), O = sum w_s acc_s / sum w_s l_s.
@@ -1389,6 +1596,15 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
                                                        vt, c, pm, pl, pacc, slots, st);
 }
 
+static bool decode_vt_staged() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = getenv("ATTN_DECODE_VT_STAGED");
+        on = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    return on == 1;
+}
+
 template <int DP>
 hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                            float *pm, float *pl, float *pacc, int Hq, int Hkv, int Sq, int Sk,
@@ -1397,6 +1613,15 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
     const long nblk = (long)Hkv * nsplit * nrb;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
+    // The staged V^T kernel's DMA offsets are 32-bit: a head's V^T must stay below 2 GiB.
+    if constexpr (DP <= 128)
+        if (vt && vec && decode_vt_staged() && (long)D * Sk * 2 < 0x7fffffffL)
+            return with_flag(causal != 0, [&](auto CA) {
+                hipLaunchKernelGGL((attn_decode_vt_kernel<DP, decltype(CA)::value>),
+                                   dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl,
+                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
+                return hipGetLastError();
+            });
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vec != 0, [&](auto VE) {
             return with_flag(vt != 0, [&](auto VTF) {
