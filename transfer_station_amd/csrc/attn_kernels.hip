@@ -1489,12 +1489,13 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 //    128-row tiles better than 256-row ones.
 //  * Otherwise 4 waves when 256-row tiles are nearly full (>= 90% of their rows are queries)
 //    but would leave CUs idle: at most half as many 8-wave workgroups as CUs, or for causal
-//    grids (uneven tiles) at most one per CU. Measured against 8 waves: 16 heads at 2k +21%,
+//    grids (uneven tiles) at most one per CU; and for causal grids whose query tiles attend
+//    at most 1024 keys on average. Measured against 8 waves: 16 heads at 2k +21%,
 //    Qwen3 causal 1k / 2k / 4k +18% / +9% / +7.5%, config 5 causal +24%. When 256-row tiles
 //    are part empty (Sq = 128, 200), 4 waves add no parallelism and their 64-key tiles lose
 //    11-20%; above the small-grid sizes 8 waves win by 5-9%.
 // ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
-static int prefill_waves(int Hq, int Hkv, int Sq, bool causal) {
+static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal) {
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
@@ -1511,7 +1512,11 @@ static int prefill_waves(int Hq, int Hkv, int Sq, bool causal) {
     const long t8 = (Sq + 255) / 256;
     const long n8 = (long)Hq * t8;
     const bool full = (long)Sq * 10 >= t8 * 256 * 9;
-    return (full && n8 <= (causal ? device_cus() : device_cus() / 2)) ? 4 : 8;
+    // Causal query tiles attend Sk - Sq/2 keys on average; up to 1024 their fixed cost per
+    // workgroup (prologue, O stores, dispatch) is large enough that two resident 4-wave
+    // workgroups per CU, which overlap it, win: c3-shaped 1k / 2k causal +15% / +3%, 4k -1%.
+    const bool short_causal = causal && (long)Sk - Sq / 2 <= 1024;
+    return (full && (n8 <= (causal ? device_cus() : device_cus() / 2) || short_causal)) ? 4 : 8;
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
@@ -1529,7 +1534,7 @@ template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
-    const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, CAUSAL) : 4;
+    const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, Sk, CAUSAL) : 4;
     // Tuning override of the key tile (the other of 64 / 128 keys), non-V^T only; the counter
     // study that fixed the defaults runs through it.
     if constexpr (DP <= 128 && KT == 128 && !VT) {
