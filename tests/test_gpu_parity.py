@@ -304,6 +304,34 @@ def test_batch_fold_bitwise_and_determinism():
         assert np.array_equal(folded[b * nq:(b + 1) * nq], one)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
+    (8, 2, 300, 1504, 128, 0),    # 8-wave workgroups, 128-key tiles
+    (8, 2, 500, 1504, 128, 1),    # 4-wave workgroups, 64-key tiles, causal
+    (8, 2, 600, 2104, 64, 0),
+    (4, 1, 1024, 1024, 128, 1),   # causal small grid: upper query tiles split over two items
+])
+def test_score_jumps_between_key_tiles(oracle, Hq, Hkv, Sq, Sk, D, causal):
+    """Each query row gets a first coordinate of +4 or -4 and each key a first coordinate that
+    steps with its 64-key block, by amounts from under the rescale margin to far past it: up
+    to 2^600 against a max from an earlier block, beyond fp32's range. Rows of either sign see
+    their maximum rise in later key tiles by every size of jump, and fall. That is the path on
+    which the running max, its rescale and the tile-sum test must all hold. Every row is
+    checked; the V^T input must give the same bits."""
+    rng = np.random.default_rng(21)
+    steps = np.array([0, 1, -3, 6, 60, 2, -40, 300, 301, 5, -300, 700, 0, 1200, 20, 1300, 8],
+                     dtype=np.float32)
+    q = oracle.bf16_to_f32(ts.synth_normal_bf16(Hq * Sq * D, 31, 0)).reshape(Hq * Sq, D)
+    q[:, 0] = np.where(rng.random(Hq * Sq) < 0.5, -4.0, 4.0)
+    k = oracle.bf16_to_f32(ts.synth_normal_bf16(Hkv * Sk * D, 31, Hq * Sq * D)).reshape(Hkv, Sk, D)
+    k[:, :, 0] = steps[(np.arange(Sk) // 64) % len(steps)]
+    Q = oracle.f32_to_bf16(q).reshape(-1)
+    K = oracle.f32_to_bf16(k).reshape(-1)
+    V = ts.synth_normal_bf16(Hkv * Sk * D, 32, 0)
+    O = check(oracle, "score jumps", Q, K, V, Hq, Hkv, Sq, Sk, D, causal)
+    Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, prepack_v=True)
+    assert np.array_equal(O, Ot)
+
+
 def test_key_permutation_invariance(oracle):
     Hq, Hkv, Sq, Sk, D = 4, 2, 64, 500, 64
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 13)

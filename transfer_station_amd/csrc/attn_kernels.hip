@@ -50,6 +50,20 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
     return (x < rem) ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
 }
 
+// xcd_remap for a grid resident all at once at two workgroups per CU (n <= 2 * CUs). Each
+// XCD hands its blocks to its R CUs in order, one slot per CU first, so XCD positions i and
+// i + R share a CU (measured with a HW_ID probe: blocks b and b + 256 on MI355X). Reversing
+// positions [R, n_x) pairs the first round's heaviest item with the second round's lightest,
+// when the logical order is heaviest first. R = 0 gives xcd_remap.
+__device__ __forceinline__ int xcd_remap_paired(int b, int n, int R) {
+    const int per = n >> 3, rem = n & 7;
+    const int x = b & 7, nx = (x < rem) ? per + 1 : per;
+    int i = b >> 3;
+    if (R > 0 && i >= R)
+        i = R + (nx - 1 - i);
+    return (x < rem) ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 __device__ __forceinline__ u32x4 zero4() {
     u32x4 z = {0u, 0u, 0u, 0u};
     return z;
@@ -371,17 +385,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 //     straight into swizzled LDS tiles (no staging registers or LDS writes).
 //   * the next 32-key sub-tile's K fragments are read from LDS between the current sub-tile's
 //     MFMAs; the row max is a max3 tree plus a VALU lane exchange (max_xor32).
-//   * lazy rescale: the running max a row subtracts is only raised when a new score exceeds it
-//     by more than kLazyLog2 (in log2 units); p is then at most 2^kLazyLog2 and the accumulator
-//     rescale (alpha != 1) runs only on those rare tiles, decided wave-uniformly. In exact
-//     arithmetic the result is identical (softmax is shift-invariant and alpha == 1 otherwise).
+//   * row max on an item's first tile only: later tiles take p against the running max m and
+//     test each lane's tile sum of p against kSumCap instead; a tile that fails is recomputed
+//     and takes the row max (softmax_next below). So every p <= kSumCap, m only rises, and the
+//     accumulator rescale (alpha != 1) runs only on those rare tiles, decided wave-uniformly.
+//     In exact arithmetic the result is identical (softmax is shift-invariant).
 //   * causal: work items are dispatched heaviest first; on grids of at most one workgroup per
 //     CU the key range of each upper-half query tile is split over two workgroups, which write
 //     partials (m, l, acc) for attn_merge2_kernel instead of O.
 //   * short query blocks under GQA (pack): the rows of a kv head's g query heads share query
 //     tiles, each lane carrying its own head and query index.
 // ------------------------------------------------------------------------------------------
-constexpr float kLazyLog2 = 8.0f;
+// Bound on a lane's tile sum of p = 2^(s c - m c) taken against a stale m (and so on each p).
+// 2^16: on peaked rows (config 5's Q ~ N(0, 16)) a cap of 2^8 / 2^12 / 2^16 sends 9.9% / 2.2% /
+// 0.13% of wave-tiles to the recompute (CPU count on the benchmark's data); N(0,1) rows never
+// reach it. p up to 2^16 costs no precision (fp32 and bf16 are relative), only 16 bits of the
+// 128-bit exponent range of the fp32 accumulators.
+constexpr float kSumCap = 65536.0f;
 
 // The descriptor must live in scalar registers; its inputs are workgroup-uniform, and the
 // readfirstlane makes that explicit so the compiler never falls back to a per-lane loop.
@@ -414,7 +434,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows, int pack) {
+    float *__restrict__ pacc, int prows, int pack, int pair_r) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -423,7 +443,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
 
     const int g = Hq / Hkv;
-    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int L = xcd_remap_paired((int)blockIdx.x, (int)gridDim.x, pair_r);
     // Work item of this workgroup: query head h, query tile qt and, for a tile whose key range
     // is split in two (causal grids too small to fill the GPU), the half `part` (-1: whole).
     // Causal work grows with the query tile, so the items of a kv head are dispatched heaviest
@@ -515,7 +535,6 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             wave_maxkey = min(Sk - 1, Sk - Sq + qmax);
     }
     const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + myq) : Sk - 1;
-    const float lazy_raw = kLazyLog2 / c; // headroom in raw-score units
 
     float m_run = kNegInf, l_run = 0.f;
     f32x16 o[DP / 32];
@@ -623,7 +642,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     bf16x8 pk[KT / 16];
     // S^T = K_tile . Q^T for one key tile (LDS buffer buf) into s; the next 32-key sub-tile's K
     // fragments are read between this sub-tile's MFMAs.
-    auto qk = [&](int buf) {
+    auto qk = [&](int buf) __attribute__((always_inline)) {
         const uint16_t *kb0 = &Ks[buf][kfo];
         bf16x8 ka[2][DP / 16];
 #pragma unroll
@@ -650,9 +669,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             }
         }
     };
-    // Online softmax of the tile at key kbase: mask, row max, lazy rescale of (l, o), then
-    // p = 2^(s c - m c) into P (bf16, the B operand of P.V) and l += sum of the fp32 p.
-    auto softmax = [&](int kbase) {
+    // Online softmax of the tile at key kbase, in three steps: mask, row max with lazy rescale of
+    // (l, o), then p = 2^(s c - m c) into P (bf16, the B operand of P.V) and the lane's sum of
+    // the fp32 p.
+    auto mask = [&](int kbase) __attribute__((always_inline)) {
         if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin)) {
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t)
@@ -663,9 +683,11 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                         s[t][i] = kNegInf;
                 }
         }
-        // Row max: one max3 chain per 32-key sub-tile (two new scores per instruction), the
-        // chains combined, the partner half-row through the VALU exchange, then the
-        // wave-uniform lazy-rescale test.
+    };
+    // Row max: one max3 chain per 32-key sub-tile (two new scores per instruction), the chains
+    // combined, the partner half-row through the VALU exchange; m rises to any larger tile max
+    // (wave-uniform test), rescaling (l, o).
+    auto row_max = [&]() __attribute__((always_inline)) {
         float mt[KT / 32];
 #pragma unroll
         for (int t = 0; t < KT / 32; ++t) {
@@ -680,7 +702,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         for (int j = 1; j < KT / 32; j += 2)
             mx = (j + 1 < KT / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
         mx = max_xor32(mx);
-        const bool raise = mx > m_run + lazy_raw;
+        const bool raise = mx > m_run;
         if (__builtin_amdgcn_ballot_w64(raise) != 0) {
             const float mnew = raise ? mx : m_run;
             const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
@@ -690,6 +712,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                 o[db] *= alpha;
             m_run = mnew;
         }
+    };
+    auto exps = [&]() __attribute__((always_inline)) -> float {
         const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
         float ps[KT / 16];
 #pragma unroll
@@ -708,7 +732,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 #pragma unroll
         for (int j = 0; j < KT / 16; ++j)
             psum += ps[j];
-        l_run += psum;
+        return psum;
     };
     // O^T += V^T . P^T for the tile in LDS buffer buf. The V^T operand of 16-key chunk cc, d
     // block db: one 16-byte read (V^T tile) or two transposed 8-byte reads (row-major V tile).
@@ -726,6 +750,27 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db)
             va[0][db] = vfrag(buf, 0, db);
+    };
+    // Softmax of a tile after an item's first. Its p are taken against the running m with no
+    // row max, and each lane's tile sum is tested instead: it bounds each of the lane's p, so a
+    // sum of at most kSumCap keeps every p <= kSumCap. A tile that fails the test (or is not
+    // finite) is recomputed from the K tile still in LDS and takes the row max, which brings
+    // that row's p back to at most 1. Either way m only rises and never falls behind a score by
+    // more than log2(kSumCap) / c. An item's first tile always takes the row max (the loop below
+    // peels it), so m starts at its tile's maximum and a row whose first tile holds its largest
+    // score keeps weight exactly 1. A row still at m = -inf after its first tile has no
+    // admissible key in the item (keys only grow along the tiles), so its p stay 0.
+    auto softmax_next = [&](int buf, int kbase) __attribute__((always_inline)) {
+        mask(kbase);
+        float psum = exps();
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(psum <= kSumCap)) != 0, 0)) {
+            qk(buf);
+            pv_first(buf); // re-read, so the earlier fragments are not live across qk
+            mask(kbase);
+            row_max();
+            psum = exps();
+        }
+        l_run += psum;
     };
     auto pv = [&](int buf) {
 #pragma unroll
@@ -756,7 +801,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // unconstrained (gfx9 encoding).
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    for (int kt = kt0; kt < kt1; ++kt) {
+    // One key tile: the next tile's DMA, then Q.K^T, softmax and P.V of this one (FIRST: the
+    // item's first tile, whose softmax takes the row max).
+    auto step = [&](int kt, auto first) __attribute__((always_inline)) {
         const int buf = (kt - kt0) & 1;
         // The other buffer's last readers finished before the barrier that ended tile kt-1.
         if (kt + 1 < kt1) {
@@ -767,12 +814,22 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         if (kbase <= wave_maxkey) {
             qk(buf);
             pv_first(buf);
-            softmax(kbase);
+            if constexpr (decltype(first)::value) {
+                mask(kbase);
+                row_max();
+                l_run += exps();
+            } else {
+                softmax_next(buf, kbase);
+            }
             pv(buf);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
         __syncthreads();
-    }
+    };
+    if (kt0 < kt1)
+        step(kt0, std::true_type{});
+    for (int kt = kt0 + 1; kt < kt1; ++kt)
+        step(kt, std::false_type{});
 
     const float lt = l_run + __shfl_xor(l_run, 32);
     if (part >= 0) {
@@ -1357,11 +1414,14 @@ __global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__rest
 // aligned: one workgroup per 64-key x 64-column tile. Key rows arrive as 16-byte loads into LDS;
 // each thread then gathers 8 consecutive keys of one column and stores them as one 16-byte
 // chunk, so each wave store writes 8 columns x 128 contiguous bytes.
+// The LDS tile has unpadded 128-byte rows, 16-byte chunk c of row r stored at chunk
+// c ^ ((r >> 3) & 7). The gathers of a wave read one column chunk of 8 rows spaced 8 apart;
+// the XOR sends those rows to 8 different chunks, so the 64 lanes touch 32 distinct banks.
 __global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__restrict__ V,
                                                             uint16_t *__restrict__ Vp, int Sk,
                                                             int D) {
-    constexpr int TK = 64, TD = 64, PITCH = TD + 8; // 144-byte rows: 16-byte aligned writes
-    __shared__ __attribute__((aligned(16))) uint16_t tile[TK * PITCH];
+    constexpr int TK = 64, TD = 64;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[TK * TD];
     const int kv = blockIdx.z;
     const int k0 = blockIdx.x * TK, d0 = blockIdx.y * TD;
     const uint16_t *src = V + (size_t)kv * Sk * D;
@@ -1375,18 +1435,20 @@ __global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__re
         u32x4 v = zero4();
         if (k < Sk && d < D)
             v = *reinterpret_cast<const u32x4 *>(src + (size_t)k * D + d);
-        *reinterpret_cast<u32x4 *>(&tile[row * PITCH + ch * 8]) = v;
+        *reinterpret_cast<u32x4 *>(&tile[row * TD + ((ch ^ (row >> 3)) & 7) * 8]) = v;
     }
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int dl = r * 32 + (tid >> 3), kc = (tid & 7) * 8;
         const int d = d0 + dl, k = k0 + kc;
+        // Rows kc .. kc+7 share (row >> 3) == tid & 7, hence one swizzled chunk.
+        const int col = (((dl >> 3) ^ (tid & 7)) & 7) * 8 + (dl & 7);
         if (d < D && k < Sk) {
             uint32_t e[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                e[j] = tile[(kc + j) * PITCH + dl];
+                e[j] = tile[(kc + j) * TD + col];
             const u32x4 out = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
                                e[6] | (e[7] << 16)};
             *reinterpret_cast<u32x4 *>(dst + (size_t)d * Sk + k) = out;
@@ -1449,6 +1511,21 @@ static int device_cus() {
 // faster, since its larger grid keeps every CU busy.
 static bool prefill_pack(int Hq, int Hkv, int Sq) { return Hq / Hkv > 1 && Sq <= 64; }
 
+// CUs per XCD for xcd_remap_paired when `on` and the n workgroups fill more than one slot per
+// CU but fit in two (all resident at once); else 0 (plain xcd_remap). ATTN_PREFILL_PAIR=0 turns
+// the pairing off for tuning sweeps.
+static int prefill_pair_r(bool on, long n) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_PAIR");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    const int cus = device_cus();
+    if (!on || !env || cus % 8 != 0 || n <= cus || n > 2L * cus)
+        return 0;
+    return cus / 8;
+}
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -1473,9 +1550,14 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
     }
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
+    // Causal items resident all at once, two per CU: pair heavy with light query tiles on each
+    // CU (xcd_remap_paired). Measured on a 16-head 4k causal grid: see prefill_pair_r.
+    const int pair_r = prefill_pair_r(CAUSAL && !pack && split_first < 0 &&
+                                          prefill_wg_per_cu(DP, KT, NW) == 2,
+                                      nblk);
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack);
+                       pl, pacc, prows, pack, pair_r);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || split_first < 0)
         return e;
