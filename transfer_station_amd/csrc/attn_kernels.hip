@@ -123,26 +123,15 @@ __device__ __forceinline__ s16x4 lds_read_tr(const uint16_t *p) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// max(a, b, c) as one v_max3_f32 (the kernels run with IEEE mode off, so no NaN quieting).
-// Written as asm: from fmaxf chains the compiler splits about half of the max3s into two v_max.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
+// max(a, b, c); with IEEE mode off the compiler emits v_max3_f32 or two v_max_f32. No inline
+// asm here on purpose: these read MFMA results, and a VALU read of an MFMA result needs wait
+// states that the hardware does not enforce; the compiler inserts them only for instructions it
+// can see (an asm v_max3 right after the last Q.K^T MFMA read stale scores).
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
-// max(x[lane], x[lane ^ 32]) in the VALU: v_permlane32_swap exchanges the upper 32 lanes of its
-// first operand with the lower 32 lanes of its second, so with both operands holding x each lane
-// ends with its partner's value in one of the two; no LDS round trip (ds_bpermute) is involved.
-// The s_nop guards cover the VALU-write -> permlane-read and permlane-write -> VALU-read
-// hazards (measured: without the leading wait states the source is read stale). Written as
-// inline asm because the compiler's folding of the builtin drops the exchange when both
-// operands are the same value.
-__device__ __forceinline__ float max_xor32(float x) {
-    float a = x, b = x;
-    asm volatile("s_nop 2\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 2" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
-}
+// max(x[lane], x[lane ^ 32]), through ds_bpermute (compiler-managed waits). The row max runs on
+// an item's first key tile and on rare recomputed tiles only, so the exchange's cost is small.
+__device__ __forceinline__ float max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 
 __device__ __forceinline__ void lds_wave_fence() {
     // Wave-private LDS reuse: finish this wave's outstanding LDS traffic and keep the compiler
@@ -483,7 +472,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             qt = split_first - 1 - ib;
         }
     }
-    const int u = h / g; // kv head
+    // Work-item values are workgroup-uniform; readfirstlane keeps them (and the loop control and
+    // tile addresses derived from them) in scalar registers, where the integer divisions above
+    // would otherwise leave them in VGPRs.
+    const int u = __builtin_amdgcn_readfirstlane(h / g); // kv head
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
@@ -534,6 +526,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         if (wvalid)
             wave_maxkey = min(Sk - 1, Sk - Sq + qmax);
     }
+    wave_maxkey = __builtin_amdgcn_readfirstlane(wave_maxkey);
+    qmin = __builtin_amdgcn_readfirstlane(qmin);
     const int lim = CAUSAL ? min(Sk - 1, Sk - Sq + myq) : Sk - 1;
 
     float m_run = kNegInf, l_run = 0.f;
@@ -626,8 +620,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const int g16 = lane >> 4, i16 = lane & 15;
 
     // Key tiles [kt0, kt1) of this item: all of them, or one half of a split tile's range.
-    const int kt0 = (part == 1) ? nkt / 2 : 0;
-    const int kt1 = (part == 0) ? nkt / 2 : nkt;
+    const int kt0 = __builtin_amdgcn_readfirstlane((part == 1) ? nkt / 2 : 0);
+    const int kt1 = __builtin_amdgcn_readfirstlane((part == 0) ? nkt / 2 : nkt);
     // Fragment offsets (elements) of this lane in a DMA-staged tile: K row t*32 + kperm,
     // chunk 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
     const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
