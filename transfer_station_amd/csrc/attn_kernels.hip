@@ -27,6 +27,7 @@
 
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "attn_flash.h"
 
@@ -62,6 +63,16 @@ __device__ __forceinline__ int xcd_remap_paired(int b, int n, int R) {
     if (R > 0 && i >= R)
         i = R + (nx - 1 - i);
     return (x < rem) ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N-1>{}): an unrolled loop
+// whose index is a constant expression (needed for sched_group_barrier counts).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F> __device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 __device__ __forceinline__ u32x4 zero4() {
@@ -379,6 +390,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 //     and takes the row max (softmax_next below). So every p <= kSumCap, m only rises, and the
 //     accumulator rescale (alpha != 1) runs only on those rare tiles, decided wave-uniformly.
 //     In exact arithmetic the result is identical (softmax is shift-invariant).
+//   * at DP = 64 such tiles without a mask are software-pipelined over their 32-key sub-tiles
+//     (tile_pipelined below): the exponentials of one sub-tile beside the MFMAs of the next
+//     sub-tile's Q.K^T and the previous one's P.V.
 //   * causal: work items are dispatched heaviest first; on grids of at most one workgroup per
 //     CU the key range of each upper-half query tile is split over two workgroups, which write
 //     partials (m, l, acc) for attn_merge2_kernel instead of O.
@@ -423,7 +437,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows, int pack, int pair_r) {
+    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -785,6 +799,125 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         }
     };
 
+    // A tile after an item's first whose keys are all admissible for the wave (no mask), software
+    // pipelined over its 32-key sub-tiles: with the row max gone from such tiles, the
+    // exponentials of sub-tile t need only t's scores, so one block issues them beside the MFMAs
+    // of Q.K^T for t+1 and P.V for t-1, and each wave overlaps its own VALU and MFMA work. Each
+    // sub-tile's p sum is tested before its P.V; a sub-tile that fails takes the row max of its
+    // own scores, rescales (l, o) and redoes its exponentials (l and o then hold sub-tiles < t
+    // only, so the rescale covers everything accumulated).
+    auto tile_pipelined = [&](int buf) __attribute__((always_inline)) {
+        constexpr int NS = KT / 32;
+        constexpr int NDB = DP / 32, NKK = DP / 16;
+        const uint16_t *kb0 = &Ks[buf][kfo];
+        bf16x8 ka[2][NKK];
+        float mc = m_run * c; // m_run is finite: every row of the wave has had an admissible key
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+            ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            s[0][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[0][kk], qb[kk], s[0], 0, 0, 0);
+            if (NS > 1)
+                ka[1][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + KSUB + kk * KDK));
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+            va[0][db] = vfrag(buf, 0, db);
+        static_for<NS>([&](auto T) __attribute__((always_inline)) {
+            constexpr int t = decltype(T)::value;
+            // MFMA work of this block: Q.K^T of sub-tile t+1 and P.V of sub-tile t-1.
+            if constexpr (t + 1 < NS) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    s[t + 1][i] = 0.f;
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    s[t + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[(t + 1) & 1][kk], qb[kk],
+                                                                       s[t + 1], 0, 0, 0);
+                    if (t + 2 < NS)
+                        ka[t & 1][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                            kb0 + (t + 2) * KSUB + kk * KDK));
+                }
+            }
+            if constexpr (t >= 1) {
+#pragma unroll
+                for (int cc = 2 * t - 2; cc < 2 * t; ++cc)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc],
+                                                                       o[db], 0, 0, 0);
+                        va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
+                    }
+            }
+            // VALU work of this block: p of sub-tile t and its sum.
+            float ps[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float p[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    p[jj] = fast_exp2(fmaf(s[t][8 * hh + jj], c, -mc));
+                    pk[2 * t + hh][jj] = (__bf16)p[jj];
+                }
+                ps[hh] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+            // Interleave: one MFMA, then its share of the LDS reads and of the VALU work.
+            constexpr int NMF = ((t + 1 < NS) ? NKK : 0) + ((t >= 1) ? 2 * NDB : 0);
+            constexpr int NDS = ((t + 2 < NS) ? NKK : 0) + ((t >= 1) ? 2 * NDB * (VT ? 1 : 2) : 0);
+            if constexpr (NMF > 0) {
+#pragma unroll
+                for (int m = 0; m < NMF; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, (NDS + NMF - 1) / NMF, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 64 / NMF, 0);
+                }
+            }
+            float psum = ps[0] + ps[1];
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(psum <= kSumCap)) != 0, 0)) {
+                float mx = max3f(s[t][0], s[t][1], s[t][2]);
+#pragma unroll
+                for (int i = 3; i < 15; i += 2)
+                    mx = max3f(mx, s[t][i], s[t][i + 1]);
+                mx = max_xor32(fmaxf(mx, s[t][15]));
+                const bool raise = mx > m_run;
+                if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+                    const float mnew = raise ? mx : m_run;
+                    const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
+                    l_run *= alpha;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+                        o[db] *= alpha;
+                    m_run = mnew;
+                    mc = m_run * c;
+                }
+                psum = 0.f;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const float p = fast_exp2(fmaf(s[t][8 * hh + jj], c, -mc));
+                        pk[2 * t + hh][jj] = (__bf16)p;
+                        psum += p;
+                    }
+            }
+            l_run += psum;
+        });
+        // P.V of the last sub-tile.
+#pragma unroll
+        for (int cc = 2 * NS - 2; cc < 2 * NS; ++cc)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], o[db], 0, 0,
+                                                               0);
+                if (cc + 1 < 2 * NS)
+                    va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
+            }
+    };
+
     if (kt0 < kt1) {
         dma_k(kt0, 0);
         dma_v(kt0, 0);
@@ -805,17 +938,25 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             dma_v(kt + 1, buf ^ 1);
         }
         const int kbase = kt * KT;
+        const bool edge = (kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin);
         if (kbase <= wave_maxkey) {
-            qk(buf);
-            pv_first(buf);
-            if constexpr (decltype(first)::value) {
-                mask(kbase);
-                row_max();
-                l_run += exps();
+            // The pipelined path at DP <= 64 only: at larger DP it spills (two sub-tiles' K
+            // fragments, S and the V read-ahead do not fit beside O and Q).
+            if (DP <= 64 && !decltype(first)::value && !edge && pipe) {
+                if constexpr (DP <= 64)
+                    tile_pipelined(buf);
             } else {
-                softmax_next(buf, kbase);
+                qk(buf);
+                pv_first(buf);
+                if constexpr (decltype(first)::value) {
+                    mask(kbase);
+                    row_max();
+                    l_run += exps();
+                } else {
+                    softmax_next(buf, kbase);
+                }
+                pv(buf);
             }
-            pv(buf);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
         __syncthreads();
@@ -1520,6 +1661,17 @@ static int prefill_pair_r(bool on, long n) {
     return cus / 8;
 }
 
+// Software-pipelined key tiles in the fast prefill kernel (tile_pipelined); ATTN_PREFILL_PIPE=0
+// (read once) turns them off for tuning sweeps.
+static int prefill_pipe() {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_PIPE");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    return env;
+}
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -1551,7 +1703,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                       nblk);
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack, pair_r);
+                       pl, pacc, prows, pack, pair_r, prefill_pipe());
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || split_first < 0)
         return e;
