@@ -304,6 +304,28 @@ def test_batch_fold_bitwise_and_determinism():
         assert np.array_equal(folded[b * nq:(b + 1) * nq], one)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal,ref_cap", [
+    (32, 8, 512, 8192, 128, 0, 8),   # chunked prefill: 128 query tiles, key range in 4 parts
+    (32, 8, 512, 8192, 128, 1, 8),   # the same, causal (the keys before the block dominate)
+    (64, 8, 128, 8192, 128, 1, 8),   # 8 parts
+    (8, 1, 1024, 8192, 128, 0, 8),   # MQA
+    (16, 4, 256, 4096, 64, 0, 0),    # D = 64 (software-pipelined tiles inside each part)
+    (8, 2, 512, 1024, 128, 1, 0),    # causal, Sk - Sq == Sq: the shortest tiles get empty parts
+    (6, 3, 200, 777, 36, 0, 0),      # general kernel (D % 8 != 0): no split, the same answer
+])
+def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
+    """Grids that fill at most half of one round of resident workgroups split each query tile's
+    key tiles into parts whose partials (m, l, acc) attn_mergew_kernel combines. Every row that
+    the reference's row set picks is checked, with the V^T input giving the same bits where
+    both inputs take the fast kernel (D % 8 == 0 and Sk % 8 == 0)."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 70 + Sq)
+    O = check(oracle, "prefill key split", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128,
+              ref_cap=ref_cap)
+    if D % 8 == 0 and Sk % 8 == 0:
+        Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, prepack_v=True)
+        assert np.array_equal(O, Ot)
+
+
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
     (8, 2, 300, 1504, 128, 0),    # 8-wave workgroups, 128-key tiles
     (8, 2, 500, 1504, 128, 1),    # 4-wave workgroups, 64-key tiles, causal

@@ -35,8 +35,9 @@ int attn_hip_static_scratch(void **ptr, size_t *bytes);
  * Split-K partial slots, one per (query row, split): m[ATTN_SLOTS], l[ATTN_SLOTS] and
  * acc[ATTN_SLOTS][D], each sub-buffer starting on a 256-byte boundary. The slot count is a
  * fixed capacity, so the size depends only on D (and trivially on bk), never on Sq/Sk; the
- * decode path caps its split count at ATTN_SLOTS / (Hq*Sq) and runs unsplit below 2, and the
- * causal prefill splits the key range of its heavier query tiles only when their rows fit. */
+ * decode path caps its split count at ATTN_SLOTS / (Hq*Sq) and runs unsplit below 2, as does
+ * the key split of an under-filled prefill grid, and the causal prefill splits the key range of
+ * its heavier query tiles only when their rows fit. */
 #define ATTN_SLOTS 65536
 #define ATTN_SUB_ALIGN 256
 

@@ -17,7 +17,8 @@
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T with the V^T tile staged in LDS
-//   attn_merge_kernel                      log-sum-exp merge of the decode partials
+//   attn_merge{2,w,}_kernel                log-sum-exp merge of split partials (2 splits / up to
+//                                          64, one wave per row / any, one workgroup per row)
 //   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
 //                                          vector path / any shape)
 // VT selects a pre-transposed V ([Hkv][D][Sk], pack_v_full's layout).
@@ -25,6 +26,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 #include <utility>
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe) {
+    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe, int nsplit) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -446,7 +448,13 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
 
     const int g = Hq / Hkv;
-    const int L = xcd_remap_paired((int)blockIdx.x, (int)gridDim.x, pair_r);
+    const int L0 = xcd_remap_paired((int)blockIdx.x, (int)gridDim.x, pair_r);
+    // Key split of an under-filled grid (nsplit > 1): item L of nit query-tile items, part sp of
+    // its key tiles. Logical ids run split-major, so the items of one kv head that read the same
+    // key range stay adjacent (one XCD, one L2 copy).
+    const int nit = (int)gridDim.x / nsplit;
+    const int sp = __builtin_amdgcn_readfirstlane(L0 / nit);
+    const int L = L0 - sp * nit;
     // Work item of this workgroup: query head h, query tile qt and, for a tile whose key range
     // is split in two (causal grids too small to fill the GPU), the half `part` (-1: whole).
     // Causal work grows with the query tile, so the items of a kv head are dispatched heaviest
@@ -634,8 +642,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const int g16 = lane >> 4, i16 = lane & 15;
 
     // Key tiles [kt0, kt1) of this item: all of them, or one half of a split tile's range.
-    const int kt0 = __builtin_amdgcn_readfirstlane((part == 1) ? nkt / 2 : 0);
-    const int kt1 = __builtin_amdgcn_readfirstlane((part == 0) ? nkt / 2 : nkt);
+    const int kt0 = __builtin_amdgcn_readfirstlane(
+        (nsplit > 1) ? (int)((long)nkt * sp / nsplit) : (part == 1) ? nkt / 2 : 0);
+    const int kt1 = __builtin_amdgcn_readfirstlane(
+        (nsplit > 1) ? (int)((long)nkt * (sp + 1) / nsplit) : (part == 0) ? nkt / 2 : nkt);
     // Fragment offsets (elements) of this lane in a DMA-staged tile: K row t*32 + kperm,
     // chunk 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
     const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
@@ -967,11 +977,13 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         step(kt, std::false_type{});
 
     const float lt = l_run + __shfl_xor(l_run, 32);
-    if (part >= 0) {
-        // Unnormalised partial of one key half: (m, l, acc) into slot (row, part) for the
-        // log-sum-exp merge (attn_merge_kernel).
+    if (part >= 0 || nsplit > 1) {
+        // Unnormalised partial of one key range: (m, l, acc) into slot (row, part) for the
+        // log-sum-exp merge (attn_merge2_kernel / attn_merge_kernel).
         if (rvalid) {
-            const size_t slot = ((size_t)h * prows + (myq - split_first * BQ)) * 2 + part;
+            const size_t slot = (nsplit > 1)
+                                    ? ((size_t)h * Sq + myq) * nsplit + sp
+                                    : ((size_t)h * prows + (myq - split_first * BQ)) * 2 + part;
             if (hi == 0) {
                 pm[slot] = m_run;
                 pl[slot] = lt;
@@ -1487,6 +1499,62 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     }
 }
 
+// 3 <= nsplit <= kMergeWaveMaxSplit (the prefill key split and short decode splits): one wave per
+// partial row, 4 rows per workgroup. Lane s holds split s's (m, l); the max and the weighted l
+// sum are wave reductions, and the final weights w_s / sum go through LDS to every lane. Columns
+// are float2 where D is even and O 8-byte aligned, so each split's columns are one coalesced
+// read per wave. Waves past the last row still reach the barrier.
+constexpr int kMergeWaveMaxSplit = 64;
+__global__ __launch_bounds__(256) void attn_mergew_kernel(const float *__restrict__ pm,
+                                                          const float *__restrict__ pl,
+                                                          const float *__restrict__ pacc,
+                                                          float *__restrict__ O, long rows, int D,
+                                                          int nsplit, float c, int rph, int q_off,
+                                                          int Sq) {
+    typedef __attribute__((ext_vector_type(2))) float f32x2;
+    __shared__ float wsh[4][kMergeWaveMaxSplit];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + wv;
+    const bool valid = row < rows;
+    const bool mine = valid && lane < nsplit;
+    const float ms = mine ? pm[row * nsplit + lane] : kNegInf;
+    float mx = ms;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float muse = (mx == kNegInf) ? 0.f : mx;
+    const float w = mine ? fast_exp2((ms - muse) * c) : 0.f;
+    float lw = mine ? w * pl[row * nsplit + lane] : 0.f;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        lw += __shfl_xor(lw, o);
+    wsh[wv][lane] = w * ((lw > 0.f) ? 1.0f / lw : 0.f);
+    __syncthreads();
+    if (!valid)
+        return;
+    const float *pr = pacc + (size_t)row * nsplit * D;
+    float *o = O + merge_orow(row, rph, q_off, Sq) * D;
+    if ((D & 1) == 0 && ((uintptr_t)O & 7u) == 0) {
+        for (int d = 2 * lane; d < D; d += 128) {
+            f32x2 acc = {0.f, 0.f};
+            for (int sp = 0; sp < nsplit; ++sp) {
+                const float a = wsh[wv][sp];
+                const f32x2 x = *reinterpret_cast<const f32x2 *>(pr + (size_t)sp * D + d);
+                acc[0] += a * x[0];
+                acc[1] += a * x[1];
+            }
+            *reinterpret_cast<f32x2 *>(o + d) = acc;
+        }
+    } else {
+        for (int d = lane; d < D; d += 64) {
+            float acc = 0.f;
+            for (int sp = 0; sp < nsplit; ++sp)
+                acc += wsh[wv][sp] * pr[(size_t)sp * D + d];
+            o[d] = acc;
+        }
+    }
+}
+
 // nsplit == 2 (the causal prefill split): one wave per partial row, 4 rows per workgroup,
 // the two weights computed once per lane, columns as float2 when D is even and O 8-byte aligned.
 __global__ __launch_bounds__(256) void attn_merge2_kernel(const float *__restrict__ pm,
@@ -1615,6 +1683,9 @@ hipError_t launch_merge(const float *pm, const float *pl, const float *pacc, flo
     if (nsplit == 2)
         hipLaunchKernelGGL(attn_merge2_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
                            pm, pl, pacc, O, rows, D, c, rph, q_off, Sq);
+    else if (nsplit <= kMergeWaveMaxSplit)
+        hipLaunchKernelGGL(attn_mergew_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                           pm, pl, pacc, O, rows, D, nsplit, c, rph, q_off, Sq);
     else if (nsplit <= kMergeMaxSplit && D <= 256)
         hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, pm, pl, pacc,
                            O, D, nsplit, c, rph, q_off, Sq);
@@ -1672,6 +1743,33 @@ static int prefill_pipe() {
     return env;
 }
 
+// Key split of a prefill grid that fills at most half of one round of resident workgroups
+// (few query tiles, long key ranges: chunked prefill, small batches): each query tile's key
+// tiles are cut into nsplit near-equal parts, run as separate workgroups that write partials
+// (m, l, acc) to the scratch, and attn_merge_kernel combines them. nsplit fills one round,
+// keeps at least kSplitMinTiles key tiles per part and fits the scratch's partial slots.
+// Causal grids take it only when the keys before the query block (Sk - Sq) are at least as many
+// as the queries, so that query tiles attend similar key counts; triangular causal grids keep
+// the split of their heavier query tiles (below). 1 = no split. ATTN_PREFILL_SPLIT=0 (read
+// once) turns it off for tuning sweeps.
+constexpr int kSplitMinTiles = 4;
+static int prefill_key_split(long nblk, int wg_per_cu, int nkt, long rows, long slots, bool ok,
+                             bool shape_ok) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_SPLIT");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    const long resident = (long)device_cus() * wg_per_cu;
+    if (!env || !ok || !shape_ok || nblk <= 0 || 2 * nblk > resident || rows <= 0)
+        return 1;
+    long ns = resident / nblk;
+    ns = std::min(ns, (long)nkt / kSplitMinTiles);
+    ns = std::min(ns, slots / rows);
+    ns = std::min(ns, (long)kMergeMaxSplit);
+    return ns >= 2 ? (int)ns : 1;
+}
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -1684,8 +1782,13 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
     const int pack = prefill_pack(Hq, Hkv, Sq) ? 1 : 0;
     const int nqt = pack ? (g * Sq + BQ - 1) / BQ : (Sq + BQ - 1) / BQ;
     long nblk = (long)(pack ? Hkv : Hq) * nqt;
+    const int nsplit = prefill_key_split(nblk, prefill_wg_per_cu(DP, KT, NW), (Sk + KT - 1) / KT,
+                                         (long)Hq * Sq, slots, pm && !pack,
+                                         !CAUSAL || (long)Sk - Sq >= Sq);
     int split_first = -1, prows = 0;
-    if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus()) {
+    if (nsplit > 1) {
+        nblk *= nsplit;
+    } else if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus()) {
         const int sf = nqt / 2;
         const long pr = (long)Sq - (long)sf * BQ;
         if (pr > 0 && 2L * Hq * pr <= slots) {
@@ -1698,14 +1801,18 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
         return hipErrorInvalidValue;
     // Causal items resident all at once, two per CU: pair heavy with light query tiles on each
     // CU (xcd_remap_paired). Measured on a 16-head 4k causal grid: see prefill_pair_r.
-    const int pair_r = prefill_pair_r(CAUSAL && !pack && split_first < 0 &&
+    const int pair_r = prefill_pair_r(CAUSAL && !pack && split_first < 0 && nsplit == 1 &&
                                           prefill_wg_per_cu(DP, KT, NW) == 2,
                                       nblk);
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack, pair_r, prefill_pipe());
+                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess || split_first < 0)
+    if (e != hipSuccess)
+        return e;
+    if (nsplit > 1)
+        return launch_merge(pm, pl, pacc, O, (long)Hq * Sq, D, nsplit, c, Sq, 0, Sq, st);
+    if (split_first < 0)
         return e;
     return launch_merge(pm, pl, pacc, O, (long)Hq * prows, D, 2, c, prows, split_first * BQ, Sq,
                         st);
