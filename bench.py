@@ -292,8 +292,10 @@ def main():
             for x in b[:4]:
                 x.free()
         # ---- config 3 at 1k/2k, config 4, config 5, config 1 --------------------------------
-        # (name, B, Hq, Hkv, Sq, Sk, D, sigma_q, seed index, bks, causal); the last one is the
-        # reference's own --long case (flash.c:1312-1314), causal, useful flops only.
+        # (name, B, Hq, Hkv, Sq, Sk, D, sigma_q, seed index, bks, causal); qwen3_4k_causal is the
+        # reference's own --long case (flash.c:1312-1314), causal, useful flops only; the last
+        # one is a serving shape outside the BASELINE configs (a 512-query chunk over 8192 keys,
+        # batch 1: few query tiles, so the key range is split over workgroups and merged).
         # bk does not select the GPU's key tile (it is fixed by D), so every bk runs one kernel:
         # a case with several bk values is timed once, at the first, and the outputs at the
         # other bk values are checked to be bit-identical to it.
@@ -302,7 +304,9 @@ def main():
                  ("c4_mqa_prefill_2k", 8, 16, 1, 2048, 2048, 128, 1.0, 4, [args.bk], 0),
                  ("c5_ragged_gqa", 2, 24, 6, 1000, 4000, 64, 4.0, 5, [128, 32, 64, 256, 512], 0),
                  ("c1_mha_256", 1, 4, 4, 256, 256, 64, 1.0, 1, [128], 0),
-                 ("qwen3_4k_causal", 1, 16, 8, 4096, 4096, 128, 1.0, 6, [args.bk], 1)]
+                 ("qwen3_4k_causal", 1, 16, 8, 4096, 4096, 128, 1.0, 6, [args.bk], 1),
+                 ("chunked_prefill_512x8192_causal", 1, 32, 8, 512, 8192, 128, 1.0, 7, [args.bk],
+                  1)]
         for name, Bc, Hqc, Hkvc, Sq, Sk, Dc, sq, ci, bks, cz in cases:
             pairs = Sq * Sk if not cz else sum(min(Sk, max(0, Sk - Sq + i + 1)) for i in range(Sq))
             fl = 4.0 * Bc * Hqc * pairs * Dc
