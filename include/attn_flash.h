@@ -14,7 +14,8 @@
  *   - The scratch keeps the reference's contract (caller-owned, size depends only on
  *     (D, bk), monotone in bk, the kernel allocates nothing and keeps no state) but its
  *     content is the GPU's: split-K partials (m, l, acc[D]), 65536 slots, for the decode
- *     path and for causal prefills too small to fill the GPU (34 MB at D = 128).
+ *     path and for prefills too small to fill the GPU, whose key ranges are split (34 MB at
+ *     D = 128).
  *   - bk is validated and sizes the scratch but does not pick the key tile: the GPU's
  *     tile is fixed by D (128 keys up to D = 128, 64 beyond), so O is bit-identical at
  *     every bk. The reference's result is bk-invariant within its tolerance.
