@@ -125,6 +125,27 @@ def test_decode_row_blocks(oracle, Hq, Hkv, Sq, Sk, D, causal):
 
 
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
+    (2048, 512, 1, 4104, 128, 0),  # 33 steps: a one-step last group, met mid-walk by most WGs
+    (8, 2, 1, 1000, 128, 0),       # 8 splits of one step each
+    (64, 16, 1, 6000, 128, 0),     # 24 splits of 2 steps, the last split one partial step
+    (512, 128, 1, 2600, 64, 1),    # D = 64: 2 tiles rows of 16; splits of 6 steps (4 + 2)
+    (256, 64, 4, 3000, 128, 1),    # 16 rows, causal mask in the last steps, 3-step splits
+    (96, 8, 4, 5000, 96, 1),       # D = 96 on 128-wide tiles, 3 row blocks
+    (40, 8, 2, 1000, 40, 0),       # D = 40 on 64-wide tiles
+])
+def test_decode_vt_groups(oracle, Hq, Hkv, Sq, Sk, D, causal):
+    """The V^T decode kernel walks the keys in groups of four 128-key steps, starting at a
+    different group per workgroup, and multiplies each group's V^T tiles one interval after
+    scoring it. Step counts that leave a partial last group (met in the middle of the walk by
+    most workgroups), splits of one to six steps, head dims that leave zero tile rows and
+    several row blocks must all give the row-major kernel's bits and the oracle's answer."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 110 + Sk)
+    O = check(oracle, "decode V^T groups", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
+    Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, prepack_v=True)
+    assert np.array_equal(O.view(np.uint32), Ot.view(np.uint32))
+
+
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
     (1024, 256, 8, 300, 64, 1),   # 32 rows per kv head, 256 kv heads: packed prefill
     (2048, 512, 16, 520, 128, 0), # 64 rows, 512 kv heads
     (1024, 256, 4, 777, 128, 1),  # 16 rows: decode at any kv-head count

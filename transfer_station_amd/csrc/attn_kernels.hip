@@ -16,7 +16,7 @@
 //                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
-//   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T with the V^T tile staged in LDS
+//   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T, staged in LDS 512 keys at a time
 //   attn_merge{2,w,}_kernel                log-sum-exp merge of split partials (2 splits / up to
 //                                          64, one wave per row / any, one workgroup per row)
 //   attn_pack_v16_kernel / attn_pack_v_kernel  V [Hkv][Sk][D] -> V^T [Hkv][D][Sk] (16-byte
@@ -1078,7 +1078,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     uint16_t *vt = &Vw[w * VTILE];
     // Each workgroup starts its walk over the 128-key steps at a different step: workgroups
     // then read different column ranges at the same time, which spreads a V^T input's
-    // 2*Sk-byte-strided rows over more HBM channels.
+    // 2*Sk-byte-strided rows over more HBM channels. attn_decode_vt_kernel walks the same order.
     const int nsteps = (k1 - k0 + 127) / 128;
     const int rot = us % (nsteps > 0 ? nsteps : 1);
     for (int js = 0; js < nsteps; ++js) {
@@ -1216,24 +1216,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
 }
 
-// Decode from V^T ([Hkv][D][Sk], D % 8 == 0, Sk % 8 == 0, 16-byte aligned tensors, DP <= 128):
-// attn_decode_kernel's workgroups, rows, S MFMAs and softmax, but the V^T operand is staged
-// through LDS. Per 128-key step the workgroup's V^T tile (DP d rows x 256 bytes) arrives by
-// LDS-DMA, each 1 KB block covering 4 d rows x 256 contiguous bytes, where loading the operand
-// layout straight from memory takes 16 d rows x 64 bytes per instruction (half lines). The 16
-// 16-byte chunks of a d row e sit at chunk slot c ^ (e % 16), so the 16 lanes of an operand
-// read (16 d rows, one key chunk) hit 16 distinct bank groups. The tile is double-buffered
-// with one barrier per step, and the next step's K fragments are loaded under this step's work.
+// Decode from V^T ([Hkv][D][Sk], D % 8 == 0, Sk % 8 == 0, 16-byte aligned tensors, DP of 64 or
+// 128): attn_decode_kernel's workgroups, rows, key order, S MFMAs and softmax, with the V^T
+// operand staged through LDS by LDS-DMA. HBM serves pieces of strided rows faster the longer
+// the piece: 128 rows 8 KB apart read in 256-byte pieces stream at about 4.7 TB/s, in 1 KB
+// pieces at about 5.9 TB/s (contiguous: 6.2). The kernel therefore walks the keys in groups of
+// 512 (four of attn_decode_kernel's 128-key steps, in its order) and stages each group's V^T
+// as four tiles of DP/4 d rows x 512 keys, every d row of a tile one 1 KB DMA. Tile i of group
+// G-1 is multiplied in the same barrier interval as step i of group G is scored, so each
+// interval has one step of K fragments and one V^T tile in flight; the softmax weights and
+// rescale factors of a group's four steps wait in registers for their tiles. Each 16-row block
+// of the output is rescaled and accumulated step by step as in attn_decode_kernel, so the two
+// kernels' outputs are bit-identical. The 16-byte chunks of a tile row e sit at slot
+// c ^ (e % 16), so the 16 lanes of an operand read (16 d rows, one key chunk) hit 16 distinct
+// bank groups.
 template <int DP, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_decode_vt_kernel(
+__global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
     float *__restrict__ pl, float *__restrict__ pacc, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nsplit, int kps, int nrb) {
-    static_assert(DP % 32 == 0 && DP <= 128, "tile shape");
-    constexpr int STEP = 128;            // keys per workgroup step: 4 waves x 32
-    constexpr int TILE = DP * STEP;      // elements of one V^T step tile
-    constexpr int NB = DP / 4, PWB = NB / 4; // 1 KB DMA blocks per tile, per wave
+    static_assert(DP == 64 || DP == 128, "tile shape");
+    constexpr int GK = 512;          // keys per group: 4 steps of 128 (4 waves x 32 keys)
+    constexpr int RQ = DP / 4;       // d rows per V^T tile
+    constexpr int RPW = RQ / 4;      // tile rows (one 1 KB DMA each) per wave
+    constexpr int DBT = RQ / 16;     // 16-row operand blocks per tile
+    constexpr int TILE = RQ * GK;    // elements of one tile
     __shared__ __attribute__((aligned(1024))) uint16_t Vt[2][TILE];
     __shared__ float red_m[4][16], red_l[4][16];
     static_assert(4 * 16 * DP * 4 <= 2 * TILE * 2, "merge area must fit in the V^T tiles");
@@ -1266,30 +1274,41 @@ __global__ __launch_bounds__(256) void attn_decode_vt_kernel(
     for (int db = 0; db < DP / 16; ++db)
         o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // This lane's DMA sources: block b = w*PWB + k holds d rows 4b .. 4b+3; lane slot p = lane%16
-    // of row e = 4b + lane/16 receives source chunk p ^ (e%16). A chunk of a d row past D or of
-    // keys at or past k1 gets an offset beyond the buffer's range and lands as zeros.
+    // This lane's DMA sources: wave w brings tile rows w*RPW .. w*RPW+RPW-1; lane slot p of
+    // tile row e receives source chunk p ^ (e % 16) (tiles start at multiples of 16 d rows, so
+    // e % 16 is also the d row's). A chunk of a d row past D or of keys at or past k1 gets an
+    // offset beyond the buffer's range and lands as zeros.
     const __amdgpu_buffer_rsrc_t rvt = make_rsrc(V + (size_t)u * D * Sk, (uint32_t)D * Sk * 2);
-    uint32_t vsrc[PWB];
-    int vkey[PWB];
+    const uint32_t row_bytes = (uint32_t)Sk * 2u;
+    uint32_t vsrc[RPW];
+    int vkey[RPW];
 #pragma unroll
-    for (int k = 0; k < PWB; ++k) {
-        const int e = 4 * (w * PWB + k) + (lane >> 4);
-        const int cs = (lane & 15) ^ (e & 15);
-        vsrc[k] = (uint32_t)e * (uint32_t)Sk * 2u + (uint32_t)cs * 16u;
-        vkey[k] = (e < D) ? cs * 8 : 0x7fffffff;
+    for (int k = 0; k < RPW; ++k) {
+        const int e = w * RPW + k;
+        const int cw = (lane ^ e) & 15; // chunk within its step; the step is lane / 16
+        vsrc[k] = (uint32_t)e * row_bytes + (uint32_t)cw * 16u;
+        vkey[k] = cw * 8;
     }
-    auto dma_step = [&](int step, int buf) {
-        const int key0 = k0 + step * STEP;
-        const int klim = k1 - key0; // keys of this step inside the split
+    // Steps in attn_decode_kernel's order (it starts at step us % nsteps), taken four at a
+    // time: group j holds walk positions 4j .. 4j+3, consecutive keys except where the walk
+    // wraps to the split's first step.
+    const int nsteps = (k1 - k0 + 127) / 128;
+    const int ngr = (nsteps + 3) / 4;
+    const int rot = us % (nsteps > 0 ? nsteps : 1);
+    auto step_of = [&](int js) { return (js + rot < nsteps) ? js + rot : js + rot - nsteps; };
+    auto dma_tile = [&](int j, int q, int buf) {
+        const int pos = 4 * j + (lane >> 4); // this lane's walk position
+        const int key0 = pos < nsteps ? k0 + step_of(pos) * 128 : k1;
+        const int klim = k1 - key0; // keys of this lane's step inside the split
+        const uint32_t base = (uint32_t)(q * RQ) * row_bytes + (uint32_t)key0 * 2u;
 #pragma unroll
-        for (int k = 0; k < PWB; ++k)
-            dma16<0>(rvt, &Vt[buf][(w * PWB + k) * 512],
-                     vkey[k] < klim ? vsrc[k] + (uint32_t)key0 * 2u : 0x80000000u);
+        for (int k = 0; k < RPW; ++k) {
+            const bool ok = q * RQ + w * RPW + k < D && vkey[k] < klim;
+            dma16<0>(rvt, &Vt[buf][(w * RPW + k) * GK], ok ? vsrc[k] + base : 0x80000000u);
+        }
     };
     u32x4 ka[2][DP / 32], kn[2][DP / 32];
-    auto load_k = [&](int step, u32x4 (&dst)[2][DP / 32]) {
-        const int tb = k0 + step * STEP + w * 32;
+    auto load_k = [&](int tb, u32x4 (&dst)[2][DP / 32]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
@@ -1299,82 +1318,109 @@ __global__ __launch_bounds__(256) void attn_decode_vt_kernel(
         }
     };
 
-    // Each workgroup starts its walk over the steps at a different step (spreads the V^T rows,
-    // 2*Sk bytes apart, over more HBM channels; see attn_decode_kernel).
-    const int nsteps = (k1 - k0 + STEP - 1) / STEP;
-    const int rot = us % (nsteps > 0 ? nsteps : 1);
-    auto step_of = [&](int js) { return (js + rot < nsteps) ? js + rot : js + rot - nsteps; };
-    if (nsteps > 0) {
-        dma_step(step_of(0), 0);
-        load_k(step_of(0), ka);
-    }
-    for (int js = 0; js < nsteps; ++js) {
-        const int buf = js & 1;
-        // This step's tile and K fragments have landed in every wave; every wave is done with
-        // the other buffer (read in step js-1).
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
-        if (js + 1 < nsteps) {
-            dma_step(step_of(js + 1), buf ^ 1);
-            load_k(step_of(js + 1), kn);
-        }
-        const int tb = k0 + step_of(js) * STEP + w * 32;
-        if (tb < k1) {
-            f32x4 s[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kk = 0; kk < DP / 32; ++kk)
-                    s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][kk]), qb[kk],
-                                                                   s[t], 0, 0, 0);
+    bf16x8 pkp[4], pkc[4]; // softmax weights of the previous / current group's steps
+    float alp[4], alc[4];  // their rescale factors
+    bool livep[4] = {false, false, false, false}, livec[4];
+    int buf = 0;
+    if (ngr > 0)
+        load_k(k0 + step_of(0) * 128 + w * 32, ka);
+    for (int j = 0; j <= ngr; ++j) {
+        const bool cur = j < ngr;
+        const int nsub = cur ? min(4, nsteps - 4 * j) : 0;
+        static_for<4>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            // What the previous interval issued (this interval's K step and V^T tile) has
+            // landed in every wave; every wave is done with the other buffer.
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+            if (i < 3) {
+                if (j > 0)
+                    dma_tile(j - 1, i + 1, buf ^ 1);
+            } else if (cur) {
+                dma_tile(j, 0, buf ^ 1);
             }
-            // Register (t, i) of this lane holds key tb + 8grp + 4t + i for row r16.
-            float mx = kNegInf;
+            int tbn = -1;
+            if (i + 1 < nsub)
+                tbn = k0 + step_of(4 * j + i + 1) * 128 + w * 32;
+            else if (i + 1 == nsub && j + 1 < ngr)
+                tbn = k0 + step_of(4 * j + 4) * 128 + w * 32;
+            if (tbn >= 0)
+                load_k(tbn, kn);
+            livec[i] = false;
+            const int tb = i < nsub ? k0 + step_of(4 * j + i) * 128 + w * 32 : k1;
+            if (tb < k1) {
+                f32x4 s[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < 2; ++t) {
+                    s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = tb + 8 * grp + 4 * t + i;
-                    if (key >= k1 || key > lim)
-                        s[t][i] = kNegInf;
-                    mx = fmaxf(mx, s[t][i]);
+                    for (int kk = 0; kk < DP / 32; ++kk)
+                        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[t][kk]),
+                                                                       qb[kk], s[t], 0, 0, 0);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(m_run, mx);
-            const float muse = (mnew == kNegInf) ? 0.f : mnew;
-            const float alpha = fast_exp2((m_run - muse) * c);
-            const float mc = muse * c;
-            float psum = 0.f;
-            bf16x8 pk;
+                // Register (t, x) of this lane holds key tb + 8grp + 4t + x for row r16.
+                float mx = kNegInf;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = fast_exp2(fmaf(s[t][i], c, -mc));
-                    psum += p;
-                    pk[4 * t + i] = (__bf16)p;
-                }
-            l_run = alpha * l_run + psum;
-            m_run = mnew;
-            // V^T operand: d row 16db + r16, keys of chunk w*4 + grp (this wave's 32 keys).
-            const int cs = w * 4 + grp;
+                    for (int x = 0; x < 4; ++x) {
+                        const int key = tb + 8 * grp + 4 * t + x;
+                        if (key >= k1 || key > lim)
+                            s[t][x] = kNegInf;
+                        mx = fmaxf(mx, s[t][x]);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float mnew = fmaxf(m_run, mx);
+                const float muse = (mnew == kNegInf) ? 0.f : mnew;
+                alc[i] = fast_exp2((m_run - muse) * c);
+                const float mc = muse * c;
+                float psum = 0.f;
 #pragma unroll
-            for (int db = 0; db < DP / 16; ++db) {
-                o[db] *= alpha;
-                const int e = db * 16 + r16;
-                const bf16x8 a = as_bf16x8(
-                    *reinterpret_cast<const u32x4 *>(&Vt[buf][e * STEP + ((cs ^ (e & 15)) * 8)]));
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        const float p = fast_exp2(fmaf(s[t][x], c, -mc));
+                        psum += p;
+                        pkc[i][4 * t + x] = (__bf16)p;
+                    }
+                l_run = alc[i] * l_run + psum;
+                m_run = mnew;
+                livec[i] = true;
             }
-        }
-        if (js + 1 < nsteps) {
+            // Tile i of the previous group: d rows i*RQ .. i*RQ+RQ-1 over its four steps.
+            if (j > 0) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+                for (int st = 0; st < 4; ++st) {
+                    if (!livep[st])
+                        continue;
+                    const int cs = st * 16 + w * 4 + grp; // this wave's 32 keys of step st
 #pragma unroll
-                for (int kk = 0; kk < DP / 32; ++kk)
-                    ka[t][kk] = kn[t][kk];
+                    for (int dl = 0; dl < DBT; ++dl) {
+                        const int db = i * DBT + dl, e = dl * 16 + r16;
+                        o[db] *= alp[st];
+                        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                            &Vt[buf][e * GK + ((cs ^ (e & 15)) * 8)]));
+                        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pkp[st], o[db], 0, 0, 0);
+                    }
+                }
+            }
+            // The next step's K fragments (waiting for them here leaves the loads in flight
+            // under both halves of the interval).
+            if (tbn >= 0) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int kk = 0; kk < DP / 32; ++kk)
+                        ka[t][kk] = kn[t][kk];
+            }
+            buf ^= 1;
+        });
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            pkp[st] = pkc[st];
+            alp[st] = alc[st];
+            livep[st] = livec[st];
         }
     }
     l_run += __shfl_xor(l_run, 16);
