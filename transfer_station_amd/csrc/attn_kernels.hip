@@ -695,8 +695,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // Online softmax of the tile at key kbase, in three steps: mask, row max with lazy rescale of
     // (l, o), then p = 2^(s c - m c) into P (bf16, the B operand of P.V) and the lane's sum of
     // the fp32 p.
-    auto mask = [&](int kbase) __attribute__((always_inline)) {
-        if ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin)) {
+    // ME (may be an edge tile) false: the tile is known to need no mask, and none is compiled.
+    auto mask = [&](int kbase, auto me) __attribute__((always_inline)) {
+        if (decltype(me)::value &&
+            ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin))) {
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t)
 #pragma unroll
@@ -783,13 +785,13 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // peels it), so m starts at its tile's maximum and a row whose first tile holds its largest
     // score keeps weight exactly 1. A row still at m = -inf after its first tile has no
     // admissible key in the item (keys only grow along the tiles), so its p stay 0.
-    auto softmax_next = [&](int buf, int kbase) __attribute__((always_inline)) {
-        mask(kbase);
+    auto softmax_next = [&](int buf, int kbase, auto me) __attribute__((always_inline)) {
+        mask(kbase, me);
         float psum = exps();
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(psum <= kSumCap)) != 0, 0)) {
             qk(buf);
             pv_first(buf); // re-read, so the earlier fragments are not live across qk
-            mask(kbase);
+            mask(kbase, me);
             row_max();
             psum = exps();
         }
@@ -944,8 +946,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     // One key tile: the next tile's DMA, then Q.K^T, softmax and P.V of this one (FIRST: the
-    // item's first tile, whose softmax takes the row max).
-    auto step = [&](int kt, auto first) __attribute__((always_inline)) {
+    // item's first tile, whose softmax takes the row max; ME: the tile may need the mask).
+    auto step = [&](int kt, auto first, auto me) __attribute__((always_inline)) {
         const int buf = (kt - kt0) & 1;
         // The other buffer's last readers finished before the barrier that ended tile kt-1.
         if (kt + 1 < kt1) {
@@ -953,7 +955,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             dma_v(kt + 1, buf ^ 1);
         }
         const int kbase = kt * KT;
-        const bool edge = (kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin);
+        const bool edge = decltype(me)::value &&
+                          ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin));
         if (kbase <= wave_maxkey) {
             // The pipelined path at DP <= 64 only: at larger DP it spills (two sub-tiles' K
             // fragments, S and the V read-ahead do not fit beside O and Q).
@@ -964,11 +967,11 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                 qk(buf);
                 pv_first(buf);
                 if constexpr (decltype(first)::value) {
-                    mask(kbase);
+                    mask(kbase, me);
                     row_max();
                     l_run += exps();
                 } else {
-                    softmax_next(buf, kbase);
+                    softmax_next(buf, kbase, me);
                 }
                 pv(buf);
             }
@@ -977,9 +980,24 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         __syncthreads();
     };
     if (kt0 < kt1)
-        step(kt0, std::true_type{});
-    for (int kt = kt0 + 1; kt < kt1; ++kt)
-        step(kt, std::false_type{});
+        step(kt0, std::true_type{}, std::true_type{});
+    if constexpr (DP <= 64) {
+        // Tiles from kt_e on may need the mask (keys past Sk, or past the causal limit of the
+        // wave's first row). The loop before them has no mask code, which keeps the masks'
+        // lane bit sets from displacing the loop's scalar registers (spill reloads per tile
+        // 20 -> 3). Measured at D = 64: c5 +3.7%, 4k +1.2%; at D = 128 the same split lost
+        // 1.3-4% (c3 4k, c3 2k, c4, c3 causal), so the wider kernels keep one loop.
+        const int medge = CAUSAL ? min(Sk - KT, Sk - Sq + qmin - KT + 1) : Sk - KT;
+        const int kt_e = __builtin_amdgcn_readfirstlane(medge < 0 ? 0 : medge / KT + 1);
+        int kt = kt0 + 1;
+        for (; kt < min(kt1, kt_e); ++kt)
+            step(kt, std::false_type{}, std::false_type{});
+        for (; kt < kt1; ++kt)
+            step(kt, std::false_type{}, std::true_type{});
+    } else {
+        for (int kt = kt0 + 1; kt < kt1; ++kt)
+            step(kt, std::false_type{}, std::true_type{});
+    }
 
     const float lt = l_run + __shfl_xor(l_run, 32);
     if (part >= 0 || nsplit > 1) {
