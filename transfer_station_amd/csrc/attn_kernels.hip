@@ -696,17 +696,31 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // (l, o), then p = 2^(s c - m c) into P (bf16, the B operand of P.V) and the lane's sum of
     // the fp32 p.
     // ME (may be an edge tile) false: the tile is known to need no mask, and none is compiled.
+    // Per 32-key sub-tile, with wave-uniform tests: the wave's smallest key limit (its first
+    // row's) leaves whole sub-tiles visible to every row, its largest (wave_maxkey) leaves whole
+    // sub-tiles visible to none; only a sub-tile between the two is masked key by key.
     auto mask = [&](int kbase, auto me) __attribute__((always_inline)) {
         if (decltype(me)::value &&
             ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin))) {
+            const int lo = CAUSAL ? min(Sk - 1, Sk - Sq + qmin) : Sk - 1;
 #pragma unroll
-            for (int t = 0; t < KT / 32; ++t)
+            for (int t = 0; t < KT / 32; ++t) {
+                const int k0t = kbase + t * 32;
+                if (k0t + 31 <= lo)
+                    continue;
+                if (k0t > wave_maxkey) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        s[t][i] = kNegInf;
+                    continue;
+                }
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int key = kbase + t * 32 + 16 * (i >> 3) + 8 * hi + (i & 7);
+                    const int key = k0t + 16 * (i >> 3) + 8 * hi + (i & 7);
                     if (key > lim)
                         s[t][i] = kNegInf;
                 }
+            }
         }
     };
     // Row max: one max3 chain per 32-key sub-tile (two new scores per instruction), the chains
