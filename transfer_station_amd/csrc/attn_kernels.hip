@@ -995,12 +995,12 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     };
     if (kt0 < kt1)
         step(kt0, std::true_type{}, std::true_type{});
-    if constexpr (DP <= 64) {
+    if constexpr (NW == 4 && DP > 64) {
         // Tiles from kt_e on may need the mask (keys past Sk, or past the causal limit of the
-        // wave's first row). The loop before them has no mask code, which keeps the masks'
-        // lane bit sets from displacing the loop's scalar registers (spill reloads per tile
-        // 20 -> 3). Measured at D = 64: c5 +3.7%, 4k +1.2%; at D = 128 the same split lost
-        // 1.3-4% (c3 4k, c3 2k, c4, c3 causal), so the wider kernels keep one loop.
+        // wave's first row); the loop before them has no mask code. Measured (same box) on the
+        // 4-wave 64-key-tile kernels: c3 1k causal +3.3%, Qwen3 4k causal +2.8%, 32 heads 2k
+        // causal +2%, 16 heads 2k +1.5%, others within 0.5%. The 8-wave kernels lost 1.5-3.5%
+        // with it (c3 4k, c3 causal, c4) and the D = 64 ones 1-2.4%, so they keep one loop.
         const int medge = CAUSAL ? min(Sk - KT, Sk - Sq + qmin - KT + 1) : Sk - KT;
         const int kt_e = __builtin_amdgcn_readfirstlane(medge < 0 ? 0 : medge / KT + 1);
         int kt = kt0 + 1;
