@@ -1039,7 +1039,45 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         return;
     }
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
-    if (rvalid) {
+    if (KT >= 16 * NW && DP <= 128 && !pack) {
+        // O leaves through LDS: the K and V tiles are idle after the key loop and hold 32 x DP
+        // fp32 per wave (waves 0 .. NW/2-1 in Ks, the others in Vs). Each wave writes its rows
+        // there in the accumulator layout (a lane pair per row) and reads them back as whole
+        // rows, so that each store instruction writes 64 consecutive 16-byte chunks of O, where
+        // the accumulator layout writes 32 rows x 32 bytes. A wave's 32 rows are consecutive rows
+        // of O (row (h*Sq + qt*BQ + w*32 + r), packed tiles included), so its block of O is one
+        // contiguous run when D == DP. Chunk c of row r sits at slot c ^ (r & SWZ): the lanes of
+        // one accumulator-layout write (32 rows, one chunk) hit distinct bank groups. At
+        // DP = 256 the staging loop's registers add spills to a kernel already at the register
+        // ceiling, and packed tiles (short, HBM-bound query blocks) lost 1-4% with the extra LDS
+        // round trip, so those store as before.
+        constexpr int NC = DP / 4; // 16-byte chunks per row
+        constexpr int SWZ = (NC % 32 == 0) ? 31 : ((NC % 16 == 0) ? 15 : 7);
+
+        float *ob = reinterpret_cast<float *>(w < NW / 2 ? &Ks[0][0] : &Vs[0][0]) +
+                    (w % (NW / 2)) * 32 * DP;
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int c = (db * 32 + i4 * 8 + 4 * hi) / 4;
+                f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
+                           o[db][4 * i4 + 3] * inv};
+                *reinterpret_cast<f32x4 *>(ob + l32 * DP + ((c ^ (l32 & SWZ)) * 4)) = v;
+            }
+        lds_wave_fence(); // this wave's rows are in LDS before any lane reads another's
+        const int row0 = qt * BQ + w * 32;        // the wave's first row in the tile's row space
+        const int rlim = pack ? g * Sq : Sq;      // rows at or past this are not queries
+        float *obase = O + ((size_t)h * Sq + (size_t)row0) * D;
+#pragma unroll
+        for (int p = 0; p < NC / 2; ++p) {
+            const int f = p * 64 + lane, r = f / NC, c = f - r * NC;
+            const f32x4 v =
+                *reinterpret_cast<const f32x4 *>(ob + r * DP + ((c ^ (r & SWZ)) * 4));
+            if (row0 + r < rlim && c * 4 < D)
+                *reinterpret_cast<f32x4 *>(obase + (size_t)r * D + c * 4) = v;
+        }
+    } else if (rvalid) {
         float *orow = O + qrow * D;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db)
