@@ -539,9 +539,34 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(V + (size_t)u * Sk * D, kvbytes); // V^T path
 
     bf16x8 qb[DP / 16];
+    // Q rows arrive either by LDS-DMA into this wave's 32 x DP block of the K/V tiles' second
+    // buffer (idle until tile kt0+1's DMA, which follows the barrier before the loop): each DMA
+    // reads 1 KB of whole rows, where loading the operand layout directly takes 32 rows x 32
+    // bytes per instruction. Chunk c of row r sits at slot c ^ (r & QSWZ), so the 32 lanes of an
+    // operand read (32 rows, one chunk) hit distinct bank groups; chunks past D and rows past Sq
+    // arrive as zeros. Measured (same box): c3 1k +1.9%, config 5 +1.9%, c3 4k causal +1.5%,
+    // c3 2k +1%, c4 +0.8%, c3 4k +0.5% with 8 waves; the 4-wave kernels measured 0 to -2%
+    // (c3 1k causal, chunked prefill), and they, packed tiles and DP = 256 load directly.
+    constexpr int NQC = DP / 8; // 16-byte chunks per Q row
+    constexpr int QSWZ = (NQC % 16 == 0) ? 15 : ((NQC % 8 == 0) ? 7 : 3);
+    const bool qstage = NW == 8 && KT >= 16 * NW && DP <= 128 && !pack &&
+                        (long)Sq * D * 2 < 0x7fffffffL;
+    const uint16_t *qlds = (w < NW / 2 ? &Ks[1][0] : &Vs[1][0]) + (w % (NW / 2)) * 32 * DP;
+    if (qstage) {
+        const __amdgpu_buffer_rsrc_t rq =
+            make_rsrc(Q + (size_t)h * Sq * D, (uint32_t)Sq * (uint32_t)D * 2u);
+        const uint32_t qr0 = (uint32_t)(qt * BQ + w * 32);
 #pragma unroll
-    for (int kk = 0; kk < DP / 16; ++kk)
-        qb[kk] = as_bf16x8(load_row8<true>(Q, qrow, kk * 16 + hi * 8, D, rvalid));
+        for (int b = 0; b < DP / 16; ++b) {
+            const int sl = b * 64 + lane, r = sl / NQC, c = (sl - r * NQC) ^ (r & QSWZ);
+            dma16<0>(rq, const_cast<uint16_t *>(qlds) + b * 512,
+                     c * 8 < D ? (qr0 + r) * (uint32_t)D * 2u + (uint32_t)c * 16u : 0x80000000u);
+        }
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+            qb[kk] = as_bf16x8(load_row8<true>(Q, qrow, kk * 16 + hi * 8, D, rvalid));
+    }
     // Q stays in flight while the first tile's DMA is issued; one wait before the loop covers
     // both (below).
 
@@ -958,6 +983,12 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // prefetch (its count cannot tell the two apart). 0x0F70 = vmcnt(0), expcnt and lgkmcnt
     // unconstrained (gfx9 encoding).
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (qstage) {
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+            qb[kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                qlds + l32 * DP + (((2 * kk + hi) ^ (l32 & QSWZ)) * 8)));
+    }
     __syncthreads();
     // One key tile: the next tile's DMA, then Q.K^T, softmax and P.V of this one (FIRST: the
     // item's first tile, whose softmax takes the row max; ME: the tile may need the mask).
