@@ -1426,7 +1426,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
 
     bf16x8 pkp[4], pkc[4]; // softmax weights of the previous / current group's steps
     float alp[4], alc[4];  // their rescale factors
-    bool livep[4] = {false, false, false, false}, livec[4];
+    int livep = 0, livec = 0; // bit st: step st of the previous / current group was scored
     int buf = 0;
     if (ngr > 0)
         load_k(k0 + step_of(0) * 128 + w * 32, ka);
@@ -1452,7 +1452,6 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
                 tbn = k0 + step_of(4 * j + 4) * 128 + w * 32;
             if (tbn >= 0)
                 load_k(tbn, kn);
-            livec[i] = false;
             const int tb = i < nsub ? k0 + step_of(4 * j + i) * 128 + w * 32 : k1;
             if (tb < k1) {
                 f32x4 s[2];
@@ -1492,13 +1491,13 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
                     }
                 l_run = alc[i] * l_run + psum;
                 m_run = mnew;
-                livec[i] = true;
+                livec |= 1 << i;
             }
             // Tile i of the previous group: d rows i*RQ .. i*RQ+RQ-1 over its four steps.
             if (j > 0) {
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    if (!livep[st])
+                    if (!(livep & (1 << st)))
                         continue;
                     const int cs = st * 16 + w * 4 + grp; // this wave's 32 keys of step st
 #pragma unroll
@@ -1526,8 +1525,9 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
         for (int st = 0; st < 4; ++st) {
             pkp[st] = pkc[st];
             alp[st] = alc[st];
-            livep[st] = livec[st];
         }
+        livep = livec;
+        livec = 0;
     }
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
