@@ -405,7 +405,8 @@ def test_bk_invariance(oracle, D, Sk):
 @pytest.mark.parametrize("Hkv,Sk,D,offset", [
     (3, 77, 40, 0),     # element-wise path (Sk % 8 != 0)
     (3, 80, 40, 0),     # 16-byte path, partial 64-column tile
-    (1, 200, 64, 0),    # 16-byte path, partial 64-key tile
+    (1, 200, 64, 0),    # 16-byte path, partial key tile (72 of 128 keys)
+    (2, 136, 96, 0),    # 16-byte path, one 8-key chunk in the last key tile, 32 of 64 columns
     (2, 4096, 128, 0),  # 16-byte path, full tiles
     (2, 8, 8, 0),       # 16-byte path, one chunk per row
     (2, 64, 64, 2),     # misaligned by one element: element-wise path

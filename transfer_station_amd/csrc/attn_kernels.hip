@@ -1766,12 +1766,12 @@ __global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__rest
 }
 
 // V [Hkv][Sk][D] -> Vp [Hkv][D][Sk] when D % 8 == 0, Sk % 8 == 0 and both tensors are 16-byte
-// aligned: one workgroup per 64-key x 64-column tile. Key rows arrive as 16-byte loads into LDS;
+// aligned: one workgroup per TK-key x 64-column tile. Key rows arrive as 16-byte loads into LDS;
 // each thread then gathers 8 consecutive keys of one column and stores them as one 16-byte
-// chunk, so each wave store writes 8 columns x 128 contiguous bytes.
+// chunk, so each wave store writes 512 / TK columns x 2*TK contiguous bytes.
 // The LDS tile has unpadded 128-byte rows, 16-byte chunk c of row r stored at chunk
-// c ^ ((r >> 3) & 7). The gathers of a wave read one column chunk of 8 rows spaced 8 apart;
-// the XOR sends those rows to 8 different chunks, so the 64 lanes touch 32 distinct banks.
+// c ^ ((r >> 3) & 7). The gathers of a wave read one column chunk of TK/8 rows spaced 8 apart;
+// the XOR sends each 8 consecutive such rows to 8 different chunks.
 template <int TK>
 __global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__restrict__ V,
                                                             uint16_t *__restrict__ Vp, int Sk,
