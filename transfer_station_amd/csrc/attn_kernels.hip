@@ -44,6 +44,24 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr float kNegInf = -__builtin_inff();
 
+// Workgroup and work-item ids read straight from their registers. HIP's blockIdx / threadIdx /
+// gridDim go through device-library functions that are built with IEEE mode on; this library
+// is built with it off (-mno-amdgpu-ieee), so the compiler will not inline them, and each use
+// would be an out-of-line call in the kernel's prologue. The workgroup count comes from the
+// kernel's own arguments instead: reading the grid size from the dispatch packet
+// (__builtin_amdgcn_grid_size_x) in every workgroup's prologue measured 2-22% slower.
+// The two kernels that stage tiles by LDS-DMA (the fast prefill and the V^T decode) still take
+// threadIdx.x, and with it one such call, on purpose. In a kernel without any call this
+// compiler makes each LDS read of a tile wait (vmcnt) for the DMA of the next tile into the
+// other buffer, which it cannot tell apart from this one: measured 3-15% slower on the prefill
+// shapes. With the call it leaves that ordering to the kernel, which does it itself (each wave
+// waits for its own DMA, vmcnt(0), before the barrier that ends a tile).
+__device__ __forceinline__ int wg_id_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int wg_id_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ int wg_id_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
+__device__ __forceinline__ int wi_id_x() { return (int)__builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int wi_id_y() { return (int)__builtin_amdgcn_workitem_id_y(); }
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Remap the
 // hardware block id so that consecutive logical ids land on the same XCD: logical ids that
 // share a kv head then share that XCD's L2 copy of K/V.
@@ -184,13 +202,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
     __shared__ __attribute__((aligned(16))) uint16_t Vs[2][VT ? DP * VTSTR : KT * VSTR];
 
     const int g = Hq / Hkv;
-    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int L = xcd_remap(wg_id_x(), Hq * nqt); // the grid is Hq * nqt workgroups
     const int u = L / (g * nqt);
     const int rr = L - u * (g * nqt);
     const int qt = rr / g;
     const int h = u * g + (rr - qt * g);
 
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = wi_id_x(), w = tid >> 6, lane = tid & 63;
     const int l32 = lane & 31, hi = lane >> 5;
     const int q0 = qt * 128 + w * 32;
     const int myq = q0 + l32;
@@ -444,7 +462,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe, int nsplit) {
+    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe, int nsplit, int nwg) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -453,11 +471,11 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
 
     const int g = Hq / Hkv;
-    const int L0 = xcd_remap_paired((int)blockIdx.x, (int)gridDim.x, pair_r);
+    const int L0 = xcd_remap_paired(wg_id_x(), nwg, pair_r); // nwg: the grid's workgroup count
     // Key split of an under-filled grid (nsplit > 1): item L of nit query-tile items, part sp of
     // its key tiles. Logical ids run split-major, so the items of one kv head that read the same
     // key range stay adjacent (one XCD, one L2 copy).
-    const int nit = (int)gridDim.x / nsplit;
+    const int nit = nwg / nsplit;
     const int sp = __builtin_amdgcn_readfirstlane(L0 / nit);
     const int L = L0 - sp * nit;
     // Work item of this workgroup: query head h, query tile qt and, for a tile whose key range
@@ -504,7 +522,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // would otherwise leave them in VGPRs.
     const int u = __builtin_amdgcn_readfirstlane(h / g); // kv head
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
     const int l32 = lane & 31, hi = lane >> 5;
     // This lane's row: query myq of head hl (valid if rvalid); the wave's valid rows have query
@@ -1154,10 +1172,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     // Row blocks of one (u, sp) are consecutive logical ids, kept on one XCD so that they share
     // its L2 copy of the K/V range.
     const int g = Hq / Hkv, M = g * Sq;
-    const int L = (nrb > 1) ? xcd_remap((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+    // The grid is Hkv * nsplit * nrb workgroups.
+    const int L = (nrb > 1) ? xcd_remap(wg_id_x(), Hkv * nsplit * nrb) : wg_id_x();
     const int rb = L % nrb, us = L / nrb;
     const int u = us / nsplit, sp = us % nsplit;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int tid = wi_id_x(), w = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, grp = lane >> 4;
     const int k0 = sp * kps, k1 = min(k0 + kps, Sk);
     const int row0 = 16 * rb, Mb = min(16, M - row0);
@@ -1353,10 +1372,11 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
     static_assert(4 * 16 * DP * 4 <= 2 * TILE * 2, "merge area must fit in the V^T tiles");
 
     const int g = Hq / Hkv, M = g * Sq;
-    const int L = (nrb > 1) ? xcd_remap((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+    // The grid is Hkv * nsplit * nrb workgroups.
+    const int L = (nrb > 1) ? xcd_remap(wg_id_x(), Hkv * nsplit * nrb) : wg_id_x();
     const int rb = L % nrb, us = L / nrb;
     const int u = us / nsplit, sp = us % nsplit;
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, grp = lane >> 4;
     const int k0 = sp * kps, k1 = min(k0 + kps, Sk);
@@ -1594,8 +1614,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     __shared__ float wsh[kMergeMaxSplit];
     __shared__ float red[256];
     __shared__ float wred[4];
-    const long row = blockIdx.x;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const long row = wg_id_x();
+    const int tid = wi_id_x(), lane = tid & 63, wv = tid >> 6;
     const size_t orow = merge_orow(row, rph, q_off, Sq);
     const float *m = pm + row * nsplit;
     const float *l = pl + row * nsplit;
@@ -1665,8 +1685,8 @@ __global__ __launch_bounds__(256) void attn_mergew_kernel(const float *__restric
                                                           int Sq) {
     typedef __attribute__((ext_vector_type(2))) float f32x2;
     __shared__ float wsh[4][kMergeWaveMaxSplit];
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + wv;
+    const int wv = wi_id_x() >> 6, lane = wi_id_x() & 63;
+    const long row = (long)wg_id_x() * 4 + wv;
     const bool valid = row < rows;
     const bool mine = valid && lane < nsplit;
     const float ms = mine ? pm[row * nsplit + lane] : kNegInf;
@@ -1715,8 +1735,8 @@ __global__ __launch_bounds__(256) void attn_merge2_kernel(const float *__restric
                                                           float *__restrict__ O, long rows, int D,
                                                           float c, int rph, int q_off, int Sq) {
     typedef __attribute__((ext_vector_type(2))) float f32x2;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const long row = (long)wg_id_x() * 4 + (wi_id_x() >> 6);
+    const int lane = wi_id_x() & 63;
     if (row >= rows)
         return;
     const size_t orow = merge_orow(row, rph, q_off, Sq);
@@ -1749,19 +1769,20 @@ __global__ __launch_bounds__(256) void attn_pack_v_kernel(const uint16_t *__rest
                                                           uint16_t *__restrict__ Vp, int Sk,
                                                           int D) {
     __shared__ uint16_t tile[32][33];
-    const int kv = blockIdx.z;
-    const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+    const int kv = wg_id_z();
+    const int k0 = wg_id_x() * 32, d0 = wg_id_y() * 32;
+    const int tx = wi_id_x(), ty = wi_id_y();
     const uint16_t *src = V + (size_t)kv * Sk * D;
     uint16_t *dst = Vp + (size_t)kv * D * Sk;
-    for (int r = threadIdx.y; r < 32; r += 8) {
-        const int k = k0 + r, d = d0 + threadIdx.x;
-        tile[r][threadIdx.x] = (k < Sk && d < D) ? src[(size_t)k * D + d] : (uint16_t)0;
+    for (int r = ty; r < 32; r += 8) {
+        const int k = k0 + r, d = d0 + tx;
+        tile[r][tx] = (k < Sk && d < D) ? src[(size_t)k * D + d] : (uint16_t)0;
     }
     __syncthreads();
-    for (int r = threadIdx.y; r < 32; r += 8) {
-        const int d = d0 + r, k = k0 + threadIdx.x;
+    for (int r = ty; r < 32; r += 8) {
+        const int d = d0 + r, k = k0 + tx;
         if (d < D && k < Sk)
-            dst[(size_t)d * Sk + k] = tile[threadIdx.x][r];
+            dst[(size_t)d * Sk + k] = tile[tx][r];
     }
 }
 
@@ -1780,11 +1801,11 @@ __global__ __launch_bounds__(256) void attn_pack_v16_kernel(const uint16_t *__re
     constexpr int TPR = TK / 8; // threads per V^T row piece (8 keys each)
     static_assert(TK % 32 == 0 && TK <= 2048, "tile");
     __shared__ __attribute__((aligned(16))) uint16_t tile[TK * TD];
-    const int kv = blockIdx.z;
-    const int k0 = blockIdx.x * TK, d0 = blockIdx.y * TD;
+    const int kv = wg_id_z();
+    const int k0 = wg_id_x() * TK, d0 = wg_id_y() * TD;
     const uint16_t *src = V + (size_t)kv * Sk * D;
     uint16_t *dst = Vp + (size_t)kv * D * Sk;
-    const int tid = threadIdx.x;
+    const int tid = wi_id_x();
 #pragma unroll
     for (int r = 0; r < TK / 32; ++r) {
         const int cidx = tid + 256 * r;
@@ -1961,7 +1982,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                       nblk);
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit);
+                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit, (int)nblk);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
