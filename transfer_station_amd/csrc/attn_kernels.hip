@@ -1039,8 +1039,13 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                 pv(buf);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): tile kt+1's DMA blocks have landed
-        __syncthreads();
+        // vmcnt(0): tile kt+1's DMA blocks have landed; the barrier publishes them and frees
+        // buffer buf for tile kt+2. After the item's last tile there is neither: its epilogue
+        // uses only the idle buffer (below), so each wave goes on without waiting for the others.
+        if (kt + 1 < kt1) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
     };
     if (kt0 < kt1)
         step(kt0, std::true_type{}, std::true_type{});
@@ -1088,45 +1093,68 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         return;
     }
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
-    if (KT >= 16 * NW && DP <= 128 && !pack) {
-        // O leaves through LDS: the K and V tiles are idle after the key loop and hold 32 x DP
-        // fp32 per wave (waves 0 .. NW/2-1 in Ks, the others in Vs). Each wave writes its rows
-        // there in the accumulator layout (a lane pair per row) and reads them back as whole
-        // rows, so that each store instruction writes 64 consecutive 16-byte chunks of O, where
-        // the accumulator layout writes 32 rows x 32 bytes. A wave's 32 rows are consecutive rows
-        // of O (row (h*Sq + qt*BQ + w*32 + r), packed tiles included), so its block of O is one
-        // contiguous run when D == DP. Chunk c of row r sits at slot c ^ (r & SWZ): the lanes of
-        // one accumulator-layout write (32 rows, one chunk) hit distinct bank groups. At
-        // DP = 256 the staging loop's registers add spills to a kernel already at the register
-        // ceiling, and packed tiles (short, HBM-bound query blocks) lost 1-4% with the extra LDS
-        // round trip, so those store as before.
-        constexpr int NC = DP / 4; // 16-byte chunks per row
-        constexpr int SWZ = (NC % 32 == 0) ? 31 : ((NC % 16 == 0) ? 15 : 7);
-
-        float *ob = reinterpret_cast<float *>(w < NW / 2 ? &Ks[0][0] : &Vs[0][0]) +
-                    (w % (NW / 2)) * 32 * DP;
+    bool staged = false;
+    if constexpr (KT >= 16 * NW && DP <= 128) {
+        if (!pack) {
+            staged = true;
+            // O leaves through LDS. Each wave writes its rows there in the accumulator layout (a
+            // lane pair per row) and reads them back as row pieces of NCP 16-byte chunks, so that
+            // each store instruction writes 64 / NCP rows x NCP consecutive chunks of O, where the
+            // accumulator layout writes 32 rows x 32 bytes. The staging area is the K/V buffer pair
+            // that the last tile left idle, (kt1 - kt0) & 1: every wave passed the barrier after
+            // its last reader, and no DMA writes it any more. So no wave waits for the others to
+            // finish the last tile: one that is done stores its rows while the others still run
+            // P.V. Each wave owns OWB bytes of it, DBP blocks of 32 columns, and stages its DP
+            // columns in passes of that width. Chunk c of row r sits at slot c ^ key(r), so that
+            // the 16 lanes of a write pass (16 rows, one chunk) or of a read pass hit 16 distinct
+            // 16-byte bank groups: with NCP % 16 == 0 every row starts at group 0 and key runs over
+            // 16 rows; with NCP % 16 == 8 rows alternate between groups 0 and 8 and key runs over
+            // row pairs. At DP = 256 the staging loop's registers add spills to a kernel already at
+            // the register ceiling, and packed tiles (short, HBM-bound query blocks) lost 1-4% with
+            // the extra LDS round trip, so those store directly.
+            constexpr int OWB = 4 * KT * DP / NW; // staging bytes per wave
+            constexpr int DBP = (OWB / 4096 < DP / 32) ? OWB / 4096 : DP / 32; // blocks per pass
+            static_assert(DBP >= 1 && DP % 32 == 0, "staging area");
+            constexpr int NCP = DBP * 8; // chunks per row piece
+            static_assert(NCP % 8 == 0, "swizzle");
+            auto key = [](int r) { return (NCP % 16 == 0) ? (r & 15) : ((r >> 1) & 7); };
+            const int nb = (kt1 - kt0) & 1;
+            float *ob = reinterpret_cast<float *>(w < NW / 2 ? &Ks[nb][0] : &Vs[nb][0]) +
+                        (w % (NW / 2)) * (OWB / 4);
+            const int row0 = qt * BQ + w * 32; // the wave's first row of the head
+            float *obase = O + ((size_t)h * Sq + (size_t)row0) * D;
 #pragma unroll
-        for (int db = 0; db < DP / 32; ++db)
+            for (int pass = 0; pass < (DP / 32 + DBP - 1) / DBP; ++pass) {
+                if (pass > 0)
+                    lds_wave_fence(); // the last pass's reads are done before its slots are reused
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const int c = (db * 32 + i4 * 8 + 4 * hi) / 4;
-                f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv, o[db][4 * i4 + 2] * inv,
-                           o[db][4 * i4 + 3] * inv};
-                *reinterpret_cast<f32x4 *>(ob + l32 * DP + ((c ^ (l32 & SWZ)) * 4)) = v;
+                for (int j = 0; j < DBP; ++j) {
+                    const int db = pass * DBP + j;
+                    if (db < DP / 32) {
+#pragma unroll
+                        for (int i4 = 0; i4 < 4; ++i4) {
+                            const int c = j * 8 + i4 * 2 + hi;
+                            f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv,
+                                       o[db][4 * i4 + 2] * inv, o[db][4 * i4 + 3] * inv};
+                            float *dst = ob + l32 * (NCP * 4) + ((c ^ key(l32)) * 4);
+                            *reinterpret_cast<f32x4 *>(dst) = v;
+                        }
+                    }
+                }
+                lds_wave_fence(); // this wave's rows are in LDS before any lane reads another's
+                const int col0 = pass * DBP * 32;
+#pragma unroll
+                for (int q = 0; q < NCP / 2; ++q) {
+                    const int f = q * 64 + lane, r = f / NCP, c = f - r * NCP;
+                    const f32x4 v =
+                        *reinterpret_cast<const f32x4 *>(ob + r * (NCP * 4) + ((c ^ key(r)) * 4));
+                    if (row0 + r < Sq && col0 + c * 4 < D)
+                        *reinterpret_cast<f32x4 *>(obase + (size_t)r * D + col0 + c * 4) = v;
+                }
             }
-        lds_wave_fence(); // this wave's rows are in LDS before any lane reads another's
-        const int row0 = qt * BQ + w * 32;        // the wave's first row in the tile's row space
-        const int rlim = pack ? g * Sq : Sq;      // rows at or past this are not queries
-        float *obase = O + ((size_t)h * Sq + (size_t)row0) * D;
-#pragma unroll
-        for (int p = 0; p < NC / 2; ++p) {
-            const int f = p * 64 + lane, r = f / NC, c = f - r * NC;
-            const f32x4 v =
-                *reinterpret_cast<const f32x4 *>(ob + r * DP + ((c ^ (r & SWZ)) * 4));
-            if (row0 + r < rlim && c * 4 < D)
-                *reinterpret_cast<f32x4 *>(obase + (size_t)r * D + c * 4) = v;
         }
-    } else if (rvalid) {
+    }
+    if (!staged && rvalid) {
         float *orow = O + qrow * D;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db)
