@@ -1181,8 +1181,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // (m, l, acc[D]) per row into the caller's scratch for attn_merge_kernel.
 // VT: V arrives as V^T ([Hkv][D][Sk]); the V^T operand (row d, 8 consecutive keys per lane) is
 // then loaded from global memory straight into its register layout, like K, with no LDS tile.
+// NTL: K and V are loaded non-temporally (decode_nt_loads decides).
 // ------------------------------------------------------------------------------------------
-template <int DP, bool CAUSAL, bool VEC, bool VT>
+template <int DP, bool CAUSAL, bool VEC, bool VT, bool NTL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
@@ -1245,20 +1246,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
 #pragma unroll
             for (int kk = 0; kk < DP / 32; ++kk)
-                ka[t][kk] = load_row8<VEC, true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+                ka[t][kk] = load_row8<VEC, NTL>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
         }
         u32x4 vv[VT ? DP / 16 : VNCH];
         if (VT) {
             // lane: d row 16db + r16, keys tb + 8grp .. +7 (the k index of pk below).
 #pragma unroll
             for (int db = 0; db < DP / 16; ++db)
-                vv[db] = load_vt8<VEC, true>(Vh, db * 16 + r16, tb + 8 * grp, Sk, D, k1);
+                vv[db] = load_vt8<VEC, NTL>(Vh, db * 16 + r16, tb + 8 * grp, Sk, D, k1);
         } else {
 #pragma unroll
             for (int r = 0; r < VNCH; ++r) {
                 const int cidx = lane + 64 * r;
                 const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-                vv[r] = load_row8<VEC, true>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
+                vv[r] = load_row8<VEC, NTL>(Vh, (size_t)(tb + row), col, D, tb + row < k1);
             }
             lds_wave_fence(); // previous tile's transposed reads are complete
 #pragma unroll
@@ -1382,8 +1383,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 // of the output is rescaled and accumulated step by step as in attn_decode_kernel, so the two
 // kernels' outputs are bit-identical. The 16-byte chunks of a tile row e sit at slot
 // c ^ (e % 16), so the 16 lanes of an operand read (16 d rows, one key chunk) hit 16 distinct
-// bank groups.
-template <int DP, bool CAUSAL>
+// bank groups. NTL: K loads and V^T DMA are non-temporal (decode_nt_loads decides).
+template <int DP, bool CAUSAL, bool NTL>
 __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, float *__restrict__ pm,
@@ -1458,7 +1459,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
             const bool ok = q * RQ + w * RPW + k < D && vkey[k] < klim;
-            dma16<0, kDmaNT>(rvt, &Vt[buf][(w * RPW + k) * GK], ok ? vsrc[k] + base : 0x80000000u);
+            dma16<0, NTL ? kDmaNT : 0>(rvt, &Vt[buf][(w * RPW + k) * GK], ok ? vsrc[k] + base : 0x80000000u);
         }
     };
     u32x4 ka[2][DP / 32], kn[2][DP / 32];
@@ -1468,7 +1469,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
             const int key = tb + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
 #pragma unroll
             for (int kk = 0; kk < DP / 32; ++kk)
-                dst[t][kk] = load_row8<true, true>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
+                dst[t][kk] = load_row8<true, NTL>(Kh, (size_t)key, kk * 32 + grp * 8, D, key < k1);
         }
     };
 
@@ -2140,6 +2141,25 @@ hipError_t launch_prefill_d(const uint16_t *Q, const uint16_t *K, const uint16_t
                                                        vt, c, pm, pl, pacc, slots, st);
 }
 
+// Non-temporal K/V loads in the decode kernels: only when every K/V byte is read by exactly one
+// workgroup (one 16-row block per kv head, nrb == 1) over a long key range (kps keys). Row
+// blocks that share a key range through L2 lose 16-31% with them (256 / 32 heads, Sq = 8,
+// Sk = 4096; 1024 / 64 heads, Sq = 4, Sk = 8192), and short ranges (512-1024 keys per
+// workgroup: 32 / 8 heads over 32768 keys, 64 / 8 heads over 65536) lose 4-6%. Long ranges of
+// 4096 keys gain 2.4-5.7% (config 2) and up to 18% at D = 64. ATTN_DECODE_NT=0 or =1 (read
+// once) forces them off or on for tuning sweeps.
+constexpr int kDecodeNTMinKeys = 2048;
+static bool decode_nt_loads(int nrb, int kps) {
+    static int forced = -2;
+    if (forced == -2) {
+        const char *e = getenv("ATTN_DECODE_NT");
+        forced = (e && (atoi(e) == 0 || atoi(e) == 1)) ? atoi(e) : -1;
+    }
+    if (forced >= 0)
+        return forced == 1;
+    return nrb == 1 && kps >= kDecodeNTMinKeys;
+}
+
 static bool decode_vt_staged() {
     static int on = -1;
     if (on < 0) {
@@ -2157,23 +2177,30 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
     const long nblk = (long)Hkv * nsplit * nrb;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
+    const bool ntl = decode_nt_loads(nrb, kps);
     // The staged V^T kernel's DMA offsets are 32-bit: a head's V^T must stay below 2 GiB.
     if constexpr (DP <= 128)
         if (vt && vec && decode_vt_staged() && (long)D * Sk * 2 < 0x7fffffffL)
             return with_flag(causal != 0, [&](auto CA) {
-                hipLaunchKernelGGL((attn_decode_vt_kernel<DP, decltype(CA)::value>),
-                                   dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl,
-                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
-                return hipGetLastError();
+                return with_flag(ntl, [&](auto NT) {
+                    hipLaunchKernelGGL(
+                        (attn_decode_vt_kernel<DP, decltype(CA)::value, decltype(NT)::value>),
+                        dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq, Hkv,
+                        Sq, Sk, D, c, nsplit, kps, nrb);
+                    return hipGetLastError();
+                });
             });
     return with_flag(causal != 0, [&](auto CA) {
         return with_flag(vec != 0, [&](auto VE) {
             return with_flag(vt != 0, [&](auto VTF) {
-                hipLaunchKernelGGL((attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
-                                                       decltype(VTF)::value>),
-                                   dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl,
-                                   pacc, Hq, Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
-                return hipGetLastError();
+                return with_flag(ntl, [&](auto NT) {
+                    hipLaunchKernelGGL(
+                        (attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
+                                            decltype(VTF)::value, decltype(NT)::value>),
+                        dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq, Hkv,
+                        Sq, Sk, D, c, nsplit, kps, nrb);
+                    return hipGetLastError();
+                });
             });
         });
     });
