@@ -560,6 +560,45 @@ def test_forced_wave_counts(waves):
     assert r.returncode == 0 and r.stdout.strip().endswith("OK")
 
 
+_DECODE_NT_SCRIPT = r"""
+import sys, numpy as np
+sys.path.insert(0, %r)
+import transfer_station_amd as ts
+out = []
+for i, (Hq, Hkv, Sq, Sk, D, causal, vt) in enumerate([(256, 64, 1, 4096, 128, 0, 0),
+                                                      (256, 32, 8, 1024, 128, 1, 0),
+                                                      (64, 8, 2, 6000, 64, 1, 0),
+                                                      (256, 64, 1, 4096, 128, 0, 1),
+                                                      (96, 8, 4, 5000, 96, 1, 1)]):
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 91 + i)
+    if vt:
+        V = np.ascontiguousarray(V.reshape(Hkv, Sk, D).transpose(0, 2, 1)).ravel()
+    out.append(ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128, v_prepacked=vt))
+np.savez(%r, *out)
+print("OK")
+"""
+
+
+def test_decode_nt_policy_is_bit_identical(tmp_path):
+    """The decode kernels' load policy (non-temporal or ordinary K/V, forced through
+    ATTN_DECODE_NT in child processes) changes caching only: O is bit-identical either way, on
+    row-block and single-block grids, row-major V and V^T."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = {}
+    for nt in ("0", "1"):
+        path = str(tmp_path / ("nt%s.npz" % nt))
+        env = dict(os.environ, ATTN_DECODE_NT=nt)
+        r = subprocess.run([sys.executable, "-c", _DECODE_NT_SCRIPT % (root, path)], env=env,
+                           capture_output=True, text=True, timeout=240)
+        say(r.stdout[-2000:] + r.stderr[-2000:])
+        assert r.returncode == 0 and r.stdout.strip().endswith("OK")
+        with np.load(path) as z:
+            res[nt] = [z[k] for k in sorted(z.files, key=lambda f: int(f.split("_")[1]))]
+    for a, b in zip(res["0"], res["1"]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 # ---- seeded random shapes over every kernel and staging path ---------------------------------
 def _random_cases(n, seed):
     rng = np.random.default_rng(seed)
