@@ -347,6 +347,25 @@ def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
         assert np.array_equal(O, Ot)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,sigma_q,ref_cap", [
+    (48, 12, 1000, 4000, 64, 4.0, 8),  # config 5: 384 tiles, the last 16 heads in key halves
+    (40, 10, 1000, 4000, 64, 1.0, 8),  # 320 tiles, 24 heads halved, 128 whole tiles
+    (20, 5, 1800, 2056, 40, 1.0, 0),   # D = 40 on the 64-wide tiles, a key tail, every row
+])
+def test_prefill_head_split(oracle, Hq, Hkv, Sq, Sk, D, sigma_q, ref_cap):
+    """Non-causal D <= 64 grids of one to two 128-row tiles per CU run the last heads' tiles as
+    two key halves merged through the scratch, whole tiles in the CUs' first slots. The rows
+    the reference's row set picks are checked against the oracle (split and whole heads alike);
+    the V^T input takes the same split and gives the same bits, and a second call repeats
+    them."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 90 + Hq, sigma_q=sigma_q)
+    O = check(oracle, "prefill head split", Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128, ref_cap=ref_cap)
+    Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, prepack_v=True)
+    assert np.array_equal(O.view(np.uint32), Ot.view(np.uint32))
+    again = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128)
+    assert np.array_equal(O.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
     (8, 2, 300, 1504, 128, 0),    # 8-wave workgroups, 128-key tiles
     (8, 2, 500, 1504, 128, 1),    # 4-wave workgroups, 64-key tiles, causal

@@ -462,7 +462,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int split_first, float *__restrict__ pm, float *__restrict__ pl,
-    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe, int nsplit, int nwg) {
+    float *__restrict__ pacc, int prows, int pack, int pair_r, int pipe, int nsplit, int nwg,
+    int hsplit) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
     constexpr int BQ = NW * 32; // query rows per workgroup
@@ -485,8 +486,29 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // pack (Sq below the workgroup's BQ rows, GQA groups): the g*Sq rows of a kv head are one
     // row space, row r being query r % Sq of head u*g + r / Sq, and qt tiles it in BQ rows, so
     // short query blocks fill whole tiles and a kv head's K/V is read once for all its heads.
-    int h, qt, part = -1;
-    if (pack) {
+    // hsplit > 0 (non-causal, two workgroups per CU, a grid of 16 R = two per CU of R CUs per
+    // XCD): the tiles of heads below Hq - hsplit run whole, in the CUs' first slots (XCD
+    // positions below R), and each tile of the last hsplit heads runs as two halves of its key
+    // range in the remaining slots, so no CU holds more than one and a half tiles.
+    int h, qt, part = -1, h0 = 0;
+    if (hsplit > 0) {
+        const int R = pair_r, b = wg_id_x(), x = b & 7, i = b >> 3;
+        const int item = (i < R) ? x * R + i : 8 * R + x * R + (i - R);
+        const int nwhole = (Hq - hsplit) * nqt;
+        if (item < nwhole) {
+            h = item / nqt;
+            qt = item - h * nqt;
+        } else {
+            const int k = item - nwhole;
+            if (k >= 2 * hsplit * nqt)
+                return; // the grid rounds the items up to two per CU
+            const int j = k >> 1;
+            h0 = Hq - hsplit;
+            h = h0 + j / nqt;
+            qt = j - (j / nqt) * nqt;
+            part = k & 1;
+        }
+    } else if (pack) {
         const int uu = L / nqt;
         qt = L - uu * nqt;
         h = uu * g;
@@ -1074,7 +1096,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         if (rvalid) {
             const size_t slot = (nsplit > 1)
                                     ? ((size_t)h * Sq + myq) * nsplit + sp
-                                    : ((size_t)h * prows + (myq - split_first * BQ)) * 2 + part;
+                                    : ((size_t)(h - h0) * prows + (myq - split_first * BQ)) * 2 +
+                                          part;
             if (hi == 0) {
                 pm[slot] = m_run;
                 pl[slot] = lt;
@@ -1975,6 +1998,35 @@ static int prefill_key_split(long nblk, int wg_per_cu, int nkt, long rows, long 
     return ns >= 2 ? (int)ns : 1;
 }
 
+// Slot-balanced head split of a non-causal grid of n = Hq * nqt 128-row (4-wave) tiles with
+// one to two tiles per CU (two such workgroups are resident per CU). Dispatched as they are,
+// n - CUs of the CUs run two tiles and the rest one, so the grid takes two tiles' time. Instead
+// every tile of the last hs heads runs as two workgroups over the halves of its key range
+// (partials merged through the scratch): the n - hs * nqt whole tiles take the CUs' first
+// slots and the halves fill the rest, so no CU runs more than one and a half tiles. hs is the
+// largest count whose items fit two per CU; it must leave at most one whole tile per CU, and
+// each half at least 2 * kSplitMinTiles key tiles. Returns hs, or 0 when it does not apply.
+// Taken at DP <= 64 only, whose 4-wave workgroups keep 128-key tiles. Measured (same box, two
+// runs each): config 5 78.5 -> 72.9 us (+7.5%), 40 heads x 1000 over 4000 keys at D = 64
+// +3-4%; with 12 key tiles (6 per half, D = 40) -10%; with the 64-key tiles of wider 4-wave
+// workgroups it lost (D = 128 -12%, D = 96 -15%).
+// ATTN_PREFILL_HSPLIT=0 (read once) turns it off for tuning sweeps.
+static int prefill_head_split(int Hq, int Sq, int nqt, int nkt, long slots, bool ok) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_HSPLIT");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    const long cus = device_cus(), n = (long)Hq * nqt;
+    if (!env || !ok || cus % 8 != 0 || nqt <= 0 || n <= cus || n >= 2 * cus ||
+        nkt < 4 * kSplitMinTiles)
+        return 0;
+    const long hs = std::min((long)Hq, (2 * cus - n) / nqt);
+    if (hs < 1 || n - hs * nqt > cus || 2 * hs * Sq > slots)
+        return 0;
+    return (int)hs;
+}
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -2002,21 +2054,37 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
             nblk = (long)Hq * (nqt + (nqt - sf));
         }
     }
+    // Non-causal grids of one to two tiles per CU: whole tiles plus halves (prefill_head_split).
+    const int hsplit =
+        (!CAUSAL && DP <= 64 && nsplit == 1 && prefill_wg_per_cu(DP, KT, NW) == 2)
+            ? prefill_head_split(Hq, Sq, nqt, (Sk + KT - 1) / KT, slots, pm && !pack)
+            : 0;
+    if (hsplit > 0) {
+        split_first = 0;
+        prows = Sq;
+        nblk = 2L * device_cus();
+    }
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
     // Causal items resident all at once, two per CU: pair heavy with light query tiles on each
-    // CU (xcd_remap_paired). Measured on a 16-head 4k causal grid: see prefill_pair_r.
-    const int pair_r = prefill_pair_r(CAUSAL && !pack && split_first < 0 && nsplit == 1 &&
-                                          prefill_wg_per_cu(DP, KT, NW) == 2,
-                                      nblk);
+    // CU (xcd_remap_paired). Measured on a 16-head 4k causal grid: see prefill_pair_r. The head
+    // split places its items by XCD position itself and takes the CUs per XCD here.
+    const int pair_r = hsplit > 0 ? device_cus() / 8
+                                  : prefill_pair_r(CAUSAL && !pack && split_first < 0 &&
+                                                       nsplit == 1 &&
+                                                       prefill_wg_per_cu(DP, KT, NW) == 2,
+                                                   nblk);
     hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit, (int)nblk);
+                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit, (int)nblk, hsplit);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     if (nsplit > 1)
         return launch_merge(pm, pl, pacc, O, (long)Hq * Sq, D, nsplit, c, Sq, 0, Sq, st);
+    if (hsplit > 0)
+        return launch_merge(pm, pl, pacc, O + (size_t)(Hq - hsplit) * Sq * D, (long)hsplit * Sq,
+                            D, 2, c, Sq, 0, Sq, st);
     if (split_first < 0)
         return e;
     return launch_merge(pm, pl, pacc, O, (long)Hq * prows, D, 2, c, prows, split_first * BQ, Sq,
@@ -2035,7 +2103,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 //    are part empty (Sq = 128, 200), 4 waves add no parallelism and their 64-key tiles lose
 //    11-20%; above the small-grid sizes 8 waves win by 5-9%.
 // ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
-static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal) {
+static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head_split) {
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
@@ -2056,7 +2124,11 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal) {
     // workgroup (prologue, O stores, dispatch) is large enough that two resident 4-wave
     // workgroups per CU, which overlap it, win: c3-shaped 1k / 2k causal +15% / +3%, 4k -1%.
     const bool short_causal = causal && (long)Sk - Sq / 2 <= 1024;
-    return (full && (n8 <= (causal ? device_cus() : device_cus() / 2) || short_causal)) ? 4 : 8;
+    // head_split: the 4-wave grid takes the slot-balanced head split (prefill_head_split).
+    return (head_split ||
+            (full && (n8 <= (causal ? device_cus() : device_cus() / 2) || short_causal)))
+               ? 4
+               : 8;
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
@@ -2074,7 +2146,11 @@ template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
                                  float *pl, float *pacc, long slots, hipStream_t st) {
-    const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, Sk, CAUSAL) : 4;
+    constexpr int KT4 = (DP > 64 && KT == 128) ? 64 : KT; // the 4-wave key tile (below)
+    const bool hs = !CAUSAL && DP <= 64 && !prefill_pack(Hq, Hkv, Sq) &&
+                    prefill_head_split(Hq, Sq, (Sq + 127) / 128, (Sk + KT4 - 1) / KT4,
+                                       pm ? slots : 0, pm != nullptr) > 0;
+    const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, Sk, CAUSAL, hs) : 4;
     // Tuning override of the key tile (the other of 64 / 128 keys), non-V^T only; the counter
     // study that fixed the defaults runs through it.
     if constexpr (DP <= 128 && KT == 128 && !VT) {
@@ -2092,7 +2168,6 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
     // 4-wave workgroups at D > 64 take 64-key tiles: at 128 keys the tiles use 96-128 KB of LDS
     // and a CU could hold only one such workgroup (one wave per SIMD). At D > 128 the O and Q
     // registers allow only one wave per SIMD anyway, so that is the only shape there.
-    constexpr int KT4 = (DP > 64 && KT == 128) ? 64 : KT;
     return launch_prefill_fast_nw<DP, KT4, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, pm,
                                                           pl, pacc, slots, st);
 }
