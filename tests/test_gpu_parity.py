@@ -347,6 +347,29 @@ def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
         assert np.array_equal(O, Ot)
 
 
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal,ref_cap", [
+    (16, 8, 4096, 4096, 128, 1, 8),   # Qwen3 4k causal: 512 tiles of 128 rows, two rounds
+    (16, 8, 4096, 4200, 128, 1, 8),   # the same with keys before the query block
+    (16, 8, 2048, 2048, 128, 0, 8),   # 256 tiles, one per CU
+    (24, 8, 1000, 1000, 128, 0, 0),   # a ragged query tail, every row
+    (16, 4, 2048, 2056, 96, 0, 8),    # the 96-wide tiles, a key tail in the second half
+    (8, 1, 1024, 8192, 128, 0, 8),    # MQA, with the key split on top (4 parts)
+])
+def test_prefill_key_halves(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
+    """Grids that would run 4-wave workgroups at D > 64 with at most one 128-row tile per CU
+    (non-causal) or exactly two (causal) run 8 waves per 128 rows instead: waves w and w + 4
+    take the two 64-key halves of every 128-key tile and combine (m, l, o) through LDS. The rows
+    the reference's row set picks are checked against the oracle; the V^T input gives the same
+    bits, and a second call repeats them."""
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 110 + Sq + Sk)
+    O = check(oracle, "prefill key halves", Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128,
+              ref_cap=ref_cap)
+    Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, prepack_v=True)
+    assert np.array_equal(O.view(np.uint32), Ot.view(np.uint32))
+    again = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
+    assert np.array_equal(O.view(np.uint32), again.view(np.uint32))
+
+
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,sigma_q,ref_cap", [
     (48, 12, 1000, 4000, 64, 4.0, 8),  # config 5: 384 tiles, the last 16 heads in key halves
     (40, 10, 1000, 4000, 64, 1.0, 8),  # 320 tiles, 24 heads halved, 128 whole tiles
@@ -566,13 +589,14 @@ print("OK")
 """
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
-def test_forced_wave_counts(waves):
-    """Both workgroup shapes of the fast kernel (4 waves x 32 rows, 8 waves x 32 rows), forced
-    through ATTN_PREFILL_WAVES in a child process, on shapes that normally take the other."""
+@pytest.mark.parametrize("waves,kh", [("4", "1"), ("4", "0"), ("8", "1")])
+def test_forced_wave_counts(waves, kh):
+    """Every workgroup shape of the fast kernel (4 waves x 32 rows, 8 waves x 32 rows, 8 waves
+    on key halves of 128 rows), forced through ATTN_PREFILL_WAVES and ATTN_PREFILL_KH in a child
+    process, on shapes that normally take another."""
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    env = dict(os.environ, ATTN_PREFILL_WAVES=waves)
+    env = dict(os.environ, ATTN_PREFILL_WAVES=waves, ATTN_PREFILL_KH=kh)
     r = subprocess.run([sys.executable, "-c", _WAVES_SCRIPT % root], env=env, capture_output=True,
                        text=True, timeout=240)
     say(r.stdout[-2000:] + r.stderr[-2000:])

@@ -457,7 +457,12 @@ constexpr int prefill_wg_per_cu(int DP, int KT, int NW) {
     return (DP > 128 || 8 * KT * DP > 80 * 1024) ? 1 : 8 / NW;
 }
 
-template <int DP, int KT, int NW, bool CAUSAL, bool VT>
+// KH (key halves, NW = 8): a workgroup of 4 * 32 query rows whose waves w and w + 4 take the
+// same rows and the two halves of every key tile (KW = KT / 2 keys each, one wave of each SIMD
+// per half), combined through LDS at the end. For grids too small for one 256-row workgroup
+// per CU, this keeps two waves per SIMD and 128-key tiles where 4-wave workgroups would take
+// 64-key tiles.
+template <int DP, int KT, int NW, bool CAUSAL, bool VT, bool KH>
 __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
@@ -466,10 +471,14 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     int hsplit) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
-    constexpr int BQ = NW * 32; // query rows per workgroup
+    static_assert(!KH || (NW == 8 && KT == 128 && DP > 64), "key halves: 8 waves, 128-key tiles");
+    constexpr int NR = KH ? NW / 2 : NW; // waves with distinct query rows
+    constexpr int KW = KH ? KT / 2 : KT; // keys of a tile that one wave takes
+    constexpr int BQ = NR * 32;         // query rows per workgroup
     // K and V (or V^T) tiles arrive by LDS-DMA in swizzled, unpadded layouts (below).
     __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
     __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
+    __shared__ float kh_ml[KH ? 2 * NR * 64 : 1]; // KH: (m, l) of each second-half lane
 
     const int g = Hq / Hkv;
     const int L0 = xcd_remap_paired(wg_id_x(), nwg, pair_r); // nwg: the grid's workgroup count
@@ -546,6 +555,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 
     const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
+    const int wr = KH ? w % NR : w; // the wave's 32-row block of the workgroup's rows
+    const int kh = KH ? w / NR : 0; // and its half of each key tile
     const int l32 = lane & 31, hi = lane >> 5;
     // This lane's row: query myq of head hl (valid if rvalid); the wave's valid rows have query
     // indices in [qmin, qmax] (causal limits), and the workgroup's at most qwg.
@@ -553,11 +564,11 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     bool rvalid, wvalid;
     if (pack) {
         const int R = g * Sq;
-        const int r = qt * BQ + w * 32 + l32;
+        const int r = qt * BQ + wr * 32 + l32;
         rvalid = r < R;
         hl = h + (rvalid ? r / Sq : 0);
         myq = rvalid ? r - (r / Sq) * Sq : 0;
-        const int r0 = qt * BQ + w * 32, r1 = min(r0 + 31, R - 1);
+        const int r0 = qt * BQ + wr * 32, r1 = min(r0 + 31, R - 1);
         wvalid = r0 < R;
         const bool one = r0 / Sq == r1 / Sq;
         qmin = one ? r0 - (r0 / Sq) * Sq : 0;
@@ -566,9 +577,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         qwg = (g0 / Sq == g1 / Sq) ? g1 - (g1 / Sq) * Sq : Sq - 1;
     } else {
         hl = h;
-        myq = qt * BQ + w * 32 + l32;
+        myq = qt * BQ + wr * 32 + l32;
         rvalid = myq < Sq;
-        qmin = qt * BQ + w * 32;
+        qmin = qt * BQ + wr * 32;
         wvalid = qmin < Sq;
         qmax = min(qmin + 31, Sq - 1);
         qwg = min(qt * BQ + BQ - 1, Sq - 1);
@@ -595,7 +606,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     if (qstage) {
         const __amdgpu_buffer_rsrc_t rq =
             make_rsrc(Q + (size_t)h * Sq * D, (uint32_t)Sq * (uint32_t)D * 2u);
-        const uint32_t qr0 = (uint32_t)(qt * BQ + w * 32);
+        const uint32_t qr0 = (uint32_t)(qt * BQ + wr * 32);
 #pragma unroll
         for (int b = 0; b < DP / 16; ++b) {
             const int sl = b * 64 + lane, r = sl / NQC, c = (sl - r * NQC) ^ (r & QSWZ);
@@ -726,33 +737,33 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                        : hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
                              (i16 & 1) * 4;
 
-    f32x16 s[KT / 32];
-    bf16x8 pk[KT / 16];
+    f32x16 s[KW / 32];
+    bf16x8 pk[KW / 16];
     // S^T = K_tile . Q^T for one key tile (LDS buffer buf) into s; the next 32-key sub-tile's K
     // fragments are read between this sub-tile's MFMAs.
     auto qk = [&](int buf) __attribute__((always_inline)) {
-        const uint16_t *kb0 = &Ks[buf][kfo];
+        const uint16_t *kb0 = &Ks[buf][kfo + kh * (KW / 32) * KSUB];
         bf16x8 ka[2][DP / 16];
 #pragma unroll
         for (int kk = 0; kk < DP / 16; ++kk)
             ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
         __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t) {
+        for (int t = 0; t < KW / 32; ++t) {
 #pragma unroll
             for (int i = 0; i < 16; ++i)
                 s[t][i] = 0.f;
 #pragma unroll
             for (int kk = 0; kk < DP / 16; ++kk) {
                 s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
-                if (t + 1 < KT / 32)
+                if (t + 1 < KW / 32)
                     ka[(t + 1) & 1][kk] = as_bf16x8(
                         *reinterpret_cast<const u32x4 *>(kb0 + (t + 1) * KSUB + kk * KDK));
             }
 #pragma unroll
             for (int kk = 0; kk < DP / 16; ++kk) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (t + 1 < KT / 32)
+                if (t + 1 < KW / 32)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
         }
@@ -766,10 +777,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // sub-tiles visible to none; only a sub-tile between the two is masked key by key.
     auto mask = [&](int kbase, auto me) __attribute__((always_inline)) {
         if (decltype(me)::value &&
-            ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin))) {
+            ((kbase + KW > Sk) || (CAUSAL && kbase + KW - 1 > Sk - Sq + qmin))) {
             const int lo = CAUSAL ? min(Sk - 1, Sk - Sq + qmin) : Sk - 1;
 #pragma unroll
-            for (int t = 0; t < KT / 32; ++t) {
+            for (int t = 0; t < KW / 32; ++t) {
                 const int k0t = kbase + t * 32;
                 if (k0t + 31 <= lo)
                     continue;
@@ -792,9 +803,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // combined, the partner half-row through the VALU exchange; m rises to any larger tile max
     // (wave-uniform test), rescaling (l, o).
     auto row_max = [&]() __attribute__((always_inline)) {
-        float mt[KT / 32];
+        float mt[KW / 32];
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t) {
+        for (int t = 0; t < KW / 32; ++t) {
             float m = max3f(s[t][0], s[t][1], s[t][2]);
 #pragma unroll
             for (int i = 3; i < 15; i += 2)
@@ -803,8 +814,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         }
         float mx = mt[0];
 #pragma unroll
-        for (int j = 1; j < KT / 32; j += 2)
-            mx = (j + 1 < KT / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
+        for (int j = 1; j < KW / 32; j += 2)
+            mx = (j + 1 < KW / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
         mx = max_xor32(mx);
         const bool raise = mx > m_run;
         if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -819,9 +830,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     };
     auto exps = [&]() __attribute__((always_inline)) -> float {
         const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
-        float ps[KT / 16];
+        float ps[KW / 16];
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t)
+        for (int t = 0; t < KW / 32; ++t)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 float p[8];
@@ -834,7 +845,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             }
         float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < KT / 16; ++j)
+        for (int j = 0; j < KW / 16; ++j)
             psum += ps[j];
         return psum;
     };
@@ -844,6 +855,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // to land in; chunk 0 is read by pv_first before the softmax, under its exponentials.
     bf16x8 va[2][DP / 32];
     auto vfrag = [&](int buf, int cc, int db) -> bf16x8 {
+        cc += kh * (KW / 16); // the wave's key half of the tile (KH)
         if (VT)
             return as_bf16x8(
                 *reinterpret_cast<const u32x4 *>(&Vs[buf][vfo + cc * 128 + db * 32 * KT]));
@@ -878,18 +890,18 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     };
     auto pv = [&](int buf) {
 #pragma unroll
-        for (int cc = 0; cc < KT / 16; ++cc) {
+        for (int cc = 0; cc < KW / 16; ++cc) {
 #pragma unroll
             for (int db = 0; db < DP / 32; ++db) {
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], o[db], 0, 0,
                                                                0);
-                if (cc + 1 < KT / 16)
+                if (cc + 1 < KW / 16)
                     va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
             }
 #pragma unroll
             for (int db = 0; db < DP / 32; ++db) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (cc + 1 < KT / 16)
+                if (cc + 1 < KW / 16)
                     __builtin_amdgcn_sched_group_barrier(0x100, VT ? 1 : 2, 0);
             }
         }
@@ -903,7 +915,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     // own scores, rescales (l, o) and redoes its exponentials (l and o then hold sub-tiles < t
     // only, so the rescale covers everything accumulated).
     auto tile_pipelined = [&](int buf) __attribute__((always_inline)) {
-        constexpr int NS = KT / 32;
+        constexpr int NS = KW / 32;
         constexpr int NDB = DP / 32, NKK = DP / 16;
         const uint16_t *kb0 = &Ks[buf][kfo];
         bf16x8 ka[2][NKK];
@@ -1039,14 +1051,14 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             dma_k(kt + 1, buf ^ 1);
             dma_v(kt + 1, buf ^ 1);
         }
-        const int kbase = kt * KT;
+        const int kbase = kt * KT + kh * KW; // this wave's keys: [kbase, kbase + KW)
         const bool edge = decltype(me)::value &&
-                          ((kbase + KT > Sk) || (CAUSAL && kbase + KT - 1 > Sk - Sq + qmin));
+                          ((kbase + KW > Sk) || (CAUSAL && kbase + KW - 1 > Sk - Sq + qmin));
         if (kbase <= wave_maxkey) {
             // The pipelined path at DP <= 64 only: at larger DP it spills (two sub-tiles' K
             // fragments, S and the V read-ahead do not fit beside O and Q).
-            if (DP <= 64 && !decltype(first)::value && !edge && pipe) {
-                if constexpr (DP <= 64)
+            if (DP <= 64 && !KH && !decltype(first)::value && !edge && pipe) {
+                if constexpr (DP <= 64 && !KH)
                     tile_pipelined(buf);
             } else {
                 qk(buf);
@@ -1089,6 +1101,48 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             step(kt, std::false_type{}, std::true_type{});
     }
 
+    if constexpr (KH) {
+        // The second-half wave of each row block hands its (m, l, o) to the first-half wave
+        // through LDS: o into the buffer pair the last tile left idle ((kt1 - kt0) & 1: past
+        // the barrier after its last reader, no DMA pending), 16-byte pieces in lane order, so
+        // each lane reads back exactly its partner lane's values (same query, same d, same key
+        // parity). After the barrier the first-half wave combines the two with log-sum-exp
+        // weights against the larger m (a half with no admissible key has m = -inf, weight 0),
+        // and only it goes on to the epilogue, which then stages O in the other buffer.
+        const int nbx = (kt1 - kt0) & 1;
+        float *xo = reinterpret_cast<float *>((wr & 2) ? &Vs[nbx][0] : &Ks[nbx][0]) +
+                    (wr & 1) * (DP / 32) * 16 * 64;
+        if (kh == 1) {
+            kh_ml[wr * 128 + lane] = m_run;
+            kh_ml[wr * 128 + 64 + lane] = l_run;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f32x4 v = {o[db][4 * i4], o[db][4 * i4 + 1], o[db][4 * i4 + 2],
+                               o[db][4 * i4 + 3]};
+                    *reinterpret_cast<f32x4 *>(xo + ((db * 4 + i4) * 64 + lane) * 4) = v;
+                }
+        }
+        __syncthreads();
+        if (kh == 1)
+            return;
+        const float m2 = kh_ml[wr * 128 + lane], l2 = kh_ml[wr * 128 + 64 + lane];
+        const float mn = fmaxf(m_run, m2);
+        const float a1 = (m_run == kNegInf) ? 0.f : fast_exp2((m_run - mn) * c);
+        const float a2 = (m2 == kNegInf) ? 0.f : fast_exp2((m2 - mn) * c);
+        l_run = l_run * a1 + l2 * a2;
+        m_run = mn;
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(xo + ((db * 4 + i4) * 64 + lane) * 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[db][4 * i4 + j] = o[db][4 * i4 + j] * a1 + v[j] * a2;
+            }
+    }
     const float lt = l_run + __shfl_xor(l_run, 32);
     if (part >= 0 || nsplit > 1) {
         // Unnormalised partial of one key range: (m, l, acc) into slot (row, part) for the
@@ -1141,10 +1195,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             constexpr int NCP = DBP * 8; // chunks per row piece
             static_assert(NCP % 8 == 0, "swizzle");
             auto key = [](int r) { return (NCP % 16 == 0) ? (r & 15) : ((r >> 1) & 7); };
-            const int nb = (kt1 - kt0) & 1;
+            const int nb = ((kt1 - kt0) & 1) ^ (KH ? 1 : 0); // KH: the idle pair holds o halves
             float *ob = reinterpret_cast<float *>(w < NW / 2 ? &Ks[nb][0] : &Vs[nb][0]) +
                         (w % (NW / 2)) * (OWB / 4);
-            const int row0 = qt * BQ + w * 32; // the wave's first row of the head
+            const int row0 = qt * BQ + wr * 32; // the wave's first row of the head
             float *obase = O + ((size_t)h * Sq + (size_t)row0) * D;
 #pragma unroll
             for (int pass = 0; pass < (DP / 32 + DBP - 1) / DBP; ++pass) {
@@ -2030,11 +2084,11 @@ static int prefill_head_split(int Hq, int Sq, int nqt, int nkt, long slots, bool
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
-template <int DP, int KT, int NW, bool CAUSAL, bool VT>
+template <int DP, int KT, int NW, bool CAUSAL, bool VT, bool KH = false>
 hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
                                   float *pm, float *pl, float *pacc, long slots, hipStream_t st) {
-    constexpr int BQ = NW * 32;
+    constexpr int BQ = (KH ? NW / 2 : NW) * 32;
     const int g = Hq / Hkv;
     const int pack = prefill_pack(Hq, Hkv, Sq) ? 1 : 0;
     const int nqt = pack ? (g * Sq + BQ - 1) / BQ : (Sq + BQ - 1) / BQ;
@@ -2074,7 +2128,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                                        nsplit == 1 &&
                                                        prefill_wg_per_cu(DP, KT, NW) == 2,
                                                    nblk);
-    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT>), dim3((unsigned)nblk),
+    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT, KH>), dim3((unsigned)nblk),
                        dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
                        pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit, (int)nblk, hsplit);
     const hipError_t e = hipGetLastError();
@@ -2131,6 +2185,26 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
                : 8;
 }
 
+// Key halves (attn_prefill_fast_kernel's KH): where 4-wave workgroups would run at D > 64, an
+// 8-wave workgroup serves the same 128 rows with 128-key tiles, each SIMD's two waves taking
+// the two halves of every tile. Taken where it measured faster (same box, two runs each):
+// non-causal grids of at most one 128-row tile per CU (16 heads at 2k 54.3 -> 39.8 us; there
+// the 4-wave grid took the key split), and causal grids of exactly two such tiles per CU,
+// which heaviest-first dispatch balances in two rounds (Qwen3 4k 89.9 -> 86.7 us). Where it
+// adds rounds it lost: c3 1k causal (1024 tiles) 53 -> 65 us, Qwen3 2k causal (256 tiles,
+// 384 with the causal key split) 37.7 -> 42.8 us, 48 heads of 1000 rows over 4000 keys at
+// D = 96 causal (384 tiles) -2 to -7%. ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
+// 64-key-tile workgroups for tuning sweeps.
+static bool prefill_kh(int Hq, int Sq, bool causal) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_KH");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    const long n = (long)Hq * ((Sq + 127) / 128), cus = device_cus();
+    return env != 0 && (causal ? n == 2 * cus : n <= cus);
+}
+
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
 // on 8-wave workgroups, or 128 keys on 4-wave workgroups at D > 64 (one such workgroup per CU).
 static int prefill_kt_forced() {
@@ -2161,6 +2235,11 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
             return launch_prefill_fast_nw<DP, 128, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
                                                                   c, pm, pl, pacc, slots, st);
     }
+    if constexpr (DP > 64 && DP <= 128 && KT == 128)
+        if (nw == 4 && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, CAUSAL))
+            return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
+                                                                       D, c, pm, pl, pacc, slots,
+                                                                       st);
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
