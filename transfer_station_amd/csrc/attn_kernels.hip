@@ -12,8 +12,9 @@
 // products s, p = 2^(s*c - m*c) equals e^(scale*s - scale*m).
 //
 // Kernels:
-//   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT>  MFMA prefill for D % 8 == 0, D <= DP in
-//                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows
+//   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT,KH>  MFMA prefill for D % 8 == 0, D <= DP in
+//                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows,
+//                                          or (KH) 8 waves over 128 rows on key-tile halves
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T, staged in LDS 512 keys at a time
@@ -421,6 +422,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 //     partials (m, l, acc) for attn_merge2_kernel instead of O.
 //   * short query blocks under GQA (pack): the rows of a kv head's g query heads share query
 //     tiles, each lane carrying its own head and query index.
+//   * grids that do not fill the GPU evenly: a key split over several workgroups (partials
+//     merged by attn_mergew_kernel), the slot-balanced head split (D <= 64: whole tiles and key
+//     halves placed by XCD position), and key halves inside one workgroup (KH, D > 64).
 // ------------------------------------------------------------------------------------------
 // Bound on a lane's tile sum of p = 2^(s c - m c) taken against a stale m (and so on each p).
 // 2^16: on peaked rows (config 5's Q ~ N(0, 16)) a cap of 2^8 / 2^12 / 2^16 sends 9.9% / 2.2% /
