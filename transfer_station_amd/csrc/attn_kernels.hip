@@ -2197,16 +2197,20 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
 // which heaviest-first dispatch balances in two rounds (Qwen3 4k 89.9 -> 86.7 us). Where it
 // adds rounds it lost: c3 1k causal (1024 tiles) 53 -> 65 us, Qwen3 2k causal (256 tiles,
 // 384 with the causal key split) 37.7 -> 42.8 us, 48 heads of 1000 rows over 4000 keys at
-// D = 96 causal (384 tiles) -2 to -7%. ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
-// 64-key-tile workgroups for tuning sweeps.
+// D = 96 causal (384 tiles) -2 to -7%. On full grids key halves everywhere (forced) lost
+// 10-18% against 256-row workgroups (c3 4k 0.975 -> 1.095 ms, c3 4k causal 0.577 -> 0.657 ms,
+// c4 0.284 -> 0.319 ms): twice the workgroups, each with its fixed cost and a merge.
+// ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
+// 64-key-tile workgroups and =2 takes key halves wherever 4 waves run at D > 64 (with
+// ATTN_PREFILL_WAVES=4: everywhere), for tuning sweeps.
 static bool prefill_kh(int Hq, int Sq, bool causal) {
     static int env = -1;
     if (env < 0) {
         const char *e = getenv("ATTN_PREFILL_KH");
-        env = (e && atoi(e) == 0) ? 0 : 1;
+        env = (e && (atoi(e) == 0 || atoi(e) == 2)) ? atoi(e) : 1;
     }
     const long n = (long)Hq * ((Sq + 127) / 128), cus = device_cus();
-    return env != 0 && (causal ? n == 2 * cus : n <= cus);
+    return env == 2 || (env == 1 && (causal ? n == 2 * cus : n <= cus));
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
