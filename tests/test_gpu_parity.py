@@ -354,10 +354,12 @@ def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     (24, 8, 1000, 1000, 128, 0, 0),   # a ragged query tail, every row
     (16, 4, 2048, 2056, 96, 0, 8),    # the 96-wide tiles, a key tail in the second half
     (8, 1, 1024, 8192, 128, 0, 8),    # MQA, with the key split on top (4 parts)
+    (16, 8, 1024, 4096, 128, 1, 8),   # causal with 3072 keys before the block: key split too
 ])
 def test_prefill_key_halves(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     """Grids that would run 4-wave workgroups at D > 64 with at most one 128-row tile per CU
-    (non-causal) or exactly two (causal) run 8 waves per 128 rows instead: waves w and w + 4
+    (non-causal, or causal with at least as many keys before the block as queries) or exactly
+    two (causal) run 8 waves per 128 rows instead: waves w and w + 4
     take the two 64-key halves of every 128-key tile and combine (m, l, o) through LDS. The rows
     the reference's row set picks are checked against the oracle; the V^T input gives the same
     bits, and a second call repeats them."""
@@ -589,11 +591,12 @@ print("OK")
 """
 
 
-@pytest.mark.parametrize("waves,kh", [("4", "1"), ("4", "0"), ("8", "1")])
+@pytest.mark.parametrize("waves,kh", [("4", "1"), ("4", "0"), ("4", "2"), ("8", "1")])
 def test_forced_wave_counts(waves, kh):
     """Every workgroup shape of the fast kernel (4 waves x 32 rows, 8 waves x 32 rows, 8 waves
     on key halves of 128 rows), forced through ATTN_PREFILL_WAVES and ATTN_PREFILL_KH in a child
-    process, on shapes that normally take another."""
+    process, on shapes that normally take another; KH=2 puts key halves under the causal key
+    split as well."""
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     env = dict(os.environ, ATTN_PREFILL_WAVES=waves, ATTN_PREFILL_KH=kh)
