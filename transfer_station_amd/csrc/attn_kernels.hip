@@ -1837,8 +1837,9 @@ __global__ __launch_bounds__(256) void attn_mergew_kernel(const float *__restric
     }
 }
 
-// nsplit == 2 (the causal prefill split): one wave per partial row, 4 rows per workgroup,
-// the two weights computed once per lane, columns as float2 when D is even and O 8-byte aligned.
+// nsplit == 2 (the causal prefill split, the head split, two-part key splits): the two
+// weights computed once per lane, columns as float4 when D % 4 == 0 and O and the partials are
+// 16-byte aligned.
 __global__ __launch_bounds__(256) void attn_merge2_kernel(const float *__restrict__ pm,
                                                           const float *__restrict__ pl,
                                                           const float *__restrict__ pacc,
