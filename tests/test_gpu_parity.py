@@ -355,11 +355,12 @@ def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     (16, 4, 2048, 2056, 96, 0, 8),    # the 96-wide tiles, a key tail in the second half
     (8, 1, 1024, 8192, 128, 0, 8),    # MQA, with the key split on top (4 parts)
     (16, 8, 1024, 4096, 128, 1, 8),   # causal with 3072 keys before the block: key split too
+    (8, 2, 2048, 2048, 128, 1, 8),    # triangular causal, 128 tiles: the causal key split too
+    (16, 8, 2048, 2048, 128, 1, 8),   # triangular causal, 256 tiles: no split (one round)
 ])
 def test_prefill_key_halves(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
-    """Grids that would run 4-wave workgroups at D > 64 with at most one 128-row tile per CU
-    (non-causal, or causal with at least as many keys before the block as queries) or exactly
-    two (causal) run 8 waves per 128 rows instead: waves w and w + 4
+    """Grids that would run 4-wave workgroups at D > 64 with at most one 128-row tile per CU,
+    or exactly two (causal), run 8 waves per 128 rows instead: waves w and w + 4
     take the two 64-key halves of every 128-key tile and combine (m, l, o) through LDS. The rows
     the reference's row set picks are checked against the oracle; the V^T input gives the same
     bits, and a second call repeats them."""

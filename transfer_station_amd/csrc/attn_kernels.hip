@@ -2116,7 +2116,13 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
     int split_first = -1, prows = 0;
     if (nsplit > 1) {
         nblk *= nsplit;
-    } else if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus()) {
+    } else if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus() &&
+               (!KH || (nblk + (long)Hq * (nqt - nqt / 2) <= device_cus() &&
+                        (Sk + KT - 1) / KT >= 4 * kSplitMinTiles))) {
+        // Key halves (8 waves per item) take the split only when the split grid still fits one
+        // round and each half keeps at least 8 key tiles: 8 heads at 2k 28.2 -> 26.2 us with it;
+        // Qwen3 2k (384 items on 256 CUs) 42 us with it, 33.8 without; Qwen3 1k (4-tile
+        // halves) 21.2 with it, 19.5 without.
         const int sf = nqt / 2;
         const long pr = (long)Sq - (long)sf * BQ;
         if (pr > 0 && 2L * Hq * pr <= slots) {
@@ -2208,10 +2214,12 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
 // non-causal grids of at most one 128-row tile per CU (16 heads at 2k 54.3 -> 39.8 us; there
 // the 4-wave grid took the key split), and causal grids of exactly two such tiles per CU,
 // which heaviest-first dispatch balances in two rounds (Qwen3 4k 89.9 -> 86.7 us), and causal
-// grids of at most one tile per CU whose keys before the query block are at least as many as
-// the queries, which take the key split like non-causal grids (16 heads of 1024 rows over 4096
-// keys 52.3 -> 48 us, 8 heads 36.5 -> 34.3 us, 512 rows over 8192 keys +1-6%, 128 or 256 rows
-// over 8k-16k keys within -1.5 to +1.5%). Where it
+// grids of at most one tile per CU: those whose keys before the query block are at least as
+// many as the queries take the key split like non-causal grids (16 heads of 1024 rows over
+// 4096 keys 52.3 -> 48 us, 8 heads 36.5 -> 34.3 us, 512 rows over 8192 keys +1-6%, 128 or 256
+// rows over 8k-16k keys within -1.5 to +1.5%), triangular ones the causal split only where it
+// pays (launch_prefill_fast_nw): Qwen3 2k 36.8 -> 33.8 us, Qwen3 1k 21.6 -> 19.5 us, 8 heads
+// at 2k 28.2 -> 26.2 us. Where it
 // adds rounds it lost: c3 1k causal (1024 tiles) 53 -> 65 us, Qwen3 2k causal (256 tiles,
 // 384 with the causal key split) 37.7 -> 42.8 us, 48 heads of 1000 rows over 4000 keys at
 // D = 96 causal (384 tiles) -2 to -7%. On full grids key halves everywhere (forced) lost
@@ -2220,15 +2228,14 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
 // ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
 // 64-key-tile workgroups and =2 takes key halves wherever 4 waves run at D > 64 (with
 // ATTN_PREFILL_WAVES=4: everywhere), for tuning sweeps.
-static bool prefill_kh(int Hq, int Sq, int Sk, bool causal) {
+static bool prefill_kh(int Hq, int Sq, bool causal) {
     static int env = -1;
     if (env < 0) {
         const char *e = getenv("ATTN_PREFILL_KH");
         env = (e && (atoi(e) == 0 || atoi(e) == 2)) ? atoi(e) : 1;
     }
     const long n = (long)Hq * ((Sq + 127) / 128), cus = device_cus();
-    const bool split_like = !causal || (long)Sk - Sq >= Sq;
-    return env == 2 || (env == 1 && (n <= cus ? split_like : causal && n == 2 * cus));
+    return env == 2 || (env == 1 && (n <= cus || (causal && n == 2 * cus)));
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
@@ -2262,7 +2269,7 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                                                   c, pm, pl, pacc, slots, st);
     }
     if constexpr (DP > 64 && DP <= 128 && KT == 128)
-        if (nw == 4 && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, Sk, CAUSAL))
+        if (nw == 4 && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, CAUSAL))
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
