@@ -2118,11 +2118,12 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
         nblk *= nsplit;
     } else if (CAUSAL && !pack && pm && nqt >= 2 && nblk <= device_cus() &&
                (!KH || (nblk + (long)Hq * (nqt - nqt / 2) <= device_cus() &&
-                        (Sk + KT - 1) / KT >= 4 * kSplitMinTiles))) {
+                        (Sk + KT - 1) / KT >= 3 * kSplitMinTiles))) {
         // Key halves (8 waves per item) take the split only when the split grid still fits one
-        // round and each half keeps at least 8 key tiles: 8 heads at 2k 28.2 -> 26.2 us with it;
-        // Qwen3 2k (384 items on 256 CUs) 42 us with it, 33.8 without; Qwen3 1k (4-tile
-        // halves) 21.2 with it, 19.5 without.
+        // round and each half keeps at least 6 key tiles: 8 heads at 2k 28.2 -> 26.2 us with it,
+        // 8 heads at 1536 +4%, 8 heads of 1500 at D = 96 +3% (against the 4-wave split); Qwen3 2k
+        // (384 items on 256 CUs) 42 us with it, 33.8 without; Qwen3 1k (4-tile halves) 21.2
+        // with it, 19.5 without. 8 heads at 1200 (10 key tiles) stays 7% behind the 4-wave split.
         const int sf = nqt / 2;
         const long pr = (long)Sq - (long)sf * BQ;
         if (pr > 0 && 2L * Hq * pr <= slots) {
