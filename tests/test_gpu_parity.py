@@ -357,6 +357,8 @@ def test_prefill_key_split(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     (16, 8, 1024, 4096, 128, 1, 8),   # causal with 3072 keys before the block: key split too
     (8, 2, 2048, 2048, 128, 1, 8),    # triangular causal, 128 tiles: the causal key split too
     (16, 8, 2048, 2048, 128, 1, 8),   # triangular causal, 256 tiles: no split (one round)
+    (32, 8, 1024, 1000, 64, 0, 8),    # D = 64 (64-key halves of 128-key tiles), a key tail
+    (16, 8, 2048, 2048, 64, 1, 8),    # D = 64, triangular causal
 ])
 def test_prefill_key_halves(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     """Grids that would run 4-wave workgroups at D > 64 with at most one 128-row tile per CU,

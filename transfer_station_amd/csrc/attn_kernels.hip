@@ -475,7 +475,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     int hsplit) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
-    static_assert(!KH || (NW == 8 && KT == 128 && DP > 64), "key halves: 8 waves, 128-key tiles");
+    static_assert(!KH || (NW == 8 && KT == 128 && DP >= 64), "key halves: 8 waves, 128-key tiles");
     constexpr int NR = KH ? NW / 2 : NW; // waves with distinct query rows
     constexpr int KW = KH ? KT / 2 : KT; // keys of a tile that one wave takes
     constexpr int BQ = NR * 32;         // query rows per workgroup
@@ -2226,17 +2226,22 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
 // D = 96 causal (384 tiles) -2 to -7%. On full grids key halves everywhere (forced) lost
 // 10-18% against 256-row workgroups (c3 4k 0.975 -> 1.095 ms, c3 4k causal 0.577 -> 0.657 ms,
 // c4 0.284 -> 0.319 ms): twice the workgroups, each with its fixed cost and a merge.
+// At D = 64 (4-wave workgroups there keep 128-key tiles, two per CU) it measured: 32 heads at
+// 1k 27.7 -> 15.7 us, 16 heads at 2k 37.4 -> 25.5 us, 24 heads of 512 rows over 4000 keys
+// +18%, 16 heads at 2k / 4k causal +14% / +7%; config 1 (two key tiles) 6.5 -> 7.0 us, so key
+// halves need at least four key tiles. Slot-balanced head-split grids keep 4 waves.
 // ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
 // 64-key-tile workgroups and =2 takes key halves wherever 4 waves run at D > 64 (with
 // ATTN_PREFILL_WAVES=4: everywhere), for tuning sweeps.
-static bool prefill_kh(int Hq, int Sq, bool causal) {
+static bool prefill_kh(int Hq, int Sq, int Sk, bool causal) {
     static int env = -1;
     if (env < 0) {
         const char *e = getenv("ATTN_PREFILL_KH");
         env = (e && (atoi(e) == 0 || atoi(e) == 2)) ? atoi(e) : 1;
     }
     const long n = (long)Hq * ((Sq + 127) / 128), cus = device_cus();
-    return env == 2 || (env == 1 && (n <= cus || (causal && n == 2 * cus)));
+    return env == 2 ||
+           (env == 1 && Sk > 3 * 128 && (n <= cus || (causal && n == 2 * cus)));
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
@@ -2269,8 +2274,8 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
             return launch_prefill_fast_nw<DP, 128, 4, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D,
                                                                   c, pm, pl, pacc, slots, st);
     }
-    if constexpr (DP > 64 && DP <= 128 && KT == 128)
-        if (nw == 4 && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, CAUSAL))
+    if constexpr (DP >= 64 && DP <= 128 && KT == 128)
+        if (nw == 4 && !hs && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, Sk, CAUSAL))
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
