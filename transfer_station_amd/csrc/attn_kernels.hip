@@ -1251,6 +1251,383 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 }
 
 // ------------------------------------------------------------------------------------------
+// Prefill, duo layout (non-causal, row-major V, 64 < D <= DP = 128, full grids). In the fast
+// kernel each wave owns 32 query rows, so every K or V fragment read from LDS (1 KB) feeds one
+// MFMA; with all 8 waves of a CU reading their fragments, the LDS, not the MFMA pipe, bounds a
+// key tile. Here the 8 waves of a workgroup serve its 256 rows as 4 pairs: waves w and w + 4
+// share the 64 rows pr*64 .. (pr = w % 4) and split the work of every 64-key step:
+//   S^T = K . Q^T    wave half kh = w / 4 takes the step's keys kh*32 .. +31 for all 64 rows:
+//                    each K fragment feeds two MFMAs (one per 32-row block);
+//   softmax          p = 2^(s c - m c) for those 64 x 32 scores, P (bf16) written to LDS;
+//   O^T += V^T.P^T   one step later (software-pipelined), each wave accumulates the 64 d columns
+//                    dh = kh of its half over all 64 keys of the step: its own P from registers,
+//                    the partner's from LDS; each V fragment feeds two MFMAs.
+// Per wave and step: 32 MFMA and 24 KB of LDS traffic (K 8, V 8, P 4 written + 4 read), against
+// 32 MFMA and 32 KB in the fast kernel. LDS: K x 2, V x 3 and P x 2 step buffers (148 KB); one
+// barrier per step publishes the next step's K/V (issued at the start of the step) and this
+// step's P. The two waves of a pair keep one running max m per row: it is set from both halves
+// on the first step; later steps test each lane's sum of p against kSumCap, and a failing wave
+// raises a workgroup flag, on which every wave recomputes that step's scores, agrees a new max
+// with its partner and redoes its exponentials before P.V consumes them. l sums each wave's own
+// keys; the pair adds its two sums at the end.
+// ------------------------------------------------------------------------------------------
+template <int DP>
+__global__ __launch_bounds__(512, 1) void attn_prefill_duo_kernel(
+    const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
+    const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
+    float c, int nqt, int nwg) {
+    static_assert(DP == 128, "two 64-column halves of D");
+    constexpr int KT = 64;  // keys per step
+    constexpr int NW = 8;   // waves
+    constexpr int BQ = 256; // query rows per workgroup
+    constexpr int NI = KT * DP / 512; // 1 KB DMA blocks per tensor and step
+    constexpr int PW = NI / NW;
+    static_assert(PW * NW == NI, "DMA blocks per wave");
+    constexpr int KSUB = 32 * DP, KDK = 128; // K fragment steps (elements): 32 keys, 16 d
+    constexpr int PBLK = 64 * 8;             // one B operand (64 lanes x 8 bf16) of P
+    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs[3][KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Ps[2][NW][4 * PBLK];
+    __shared__ float xm[NW][128]; // row maxima, and at the end row sums, for the partner
+    __shared__ int dflag[2];      // step t + 1 when a wave's p of step t failed the sum test
+
+    const int g = Hq / Hkv;
+    const int L = xcd_remap(wg_id_x(), nwg);
+    const int uu = L / (g * nqt);
+    const int rr = L - uu * (g * nqt);
+    const int qt = rr / g;
+    const int h = uu * g + (rr - qt * g);
+    const int u = __builtin_amdgcn_readfirstlane(h / g); // kv head
+
+    const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pr = w & 3, kh = w >> 2; // row block pair, key half (and d half) of the wave
+    const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
+    const int row0 = qt * BQ + pr * 64; // the pair's first row
+
+    bf16x8 qb[2][DP / 16];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int q = row0 + rb * 32 + l32;
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+            qb[rb][kk] = as_bf16x8(load_row8<true>(Q, (size_t)h * Sq + (size_t)(q < Sq ? q : 0),
+                                                   kk * 16 + hi * 8, D, q < Sq));
+    }
+
+    // DMA source offsets of this wave's blocks of a K or V step tile (layouts as in
+    // attn_prefill_fast_kernel; a chunk of columns D and beyond arrives as zero).
+    const uint32_t kvbytes = (uint32_t)Sk * D * 2;
+    uint32_t kso[PW], vso[PW];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int b = (w * PW + k) * 1024 + 16 * lane;
+        {
+            const int rg = b / (16 * DP), wi = b % (16 * DP);
+            const int r = rg * 8 + (wi % 256) / 32;
+            const int cc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
+            kso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
+        }
+        {
+            const int rgv = b / (8 * DP), wi = b % (8 * DP);
+            const int r = rgv * 4 + (wi % 256) / 64;
+            const int cc = 4 * (wi / 256) + (wi % 64) / 16;
+            vso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
+        }
+    }
+    auto dma_k = [&](int kt, int buf) {
+        const uint32_t toff = (uint32_t)kt * KT * D * 2;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(K + (size_t)u * Sk * D + (size_t)kt * KT * D,
+                                                   kvbytes - toff);
+#pragma unroll
+        for (int k = 0; k < PW; ++k)
+            dma16<0>(r, &Ks[buf][(w * PW + k) * 512], kso[k]);
+    };
+    auto dma_v = [&](int kt, int buf) {
+        const uint32_t toff = (uint32_t)kt * KT * D * 2;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D,
+                                                   kvbytes - toff);
+#pragma unroll
+        for (int k = 0; k < PW; ++k)
+            dma16<0>(r, &Vs[buf][(w * PW + k) * 512], vso[k]);
+    };
+
+    // Fragment offsets (elements), as in attn_prefill_fast_kernel: K row kh*32 + kperm, chunk
+    // 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
+    const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8) +
+                    kh * KSUB;
+    const int vfo = hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
+                    (i16 & 1) * 4;
+
+    const int nkt = (Sk + KT - 1) / KT;
+    float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f}, ps_prev[2] = {0.f, 0.f};
+    f32x16 o[2][2]; // [d block of the wave's half][row block]
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                o[db][rb][i] = 0.f;
+    f32x16 s[2];
+
+    // S^T for the wave's 32 keys of step tile kbuf and both row blocks; K fragments are read
+    // KA - 1 16-d steps ahead (each feeds two MFMAs).
+    auto qk2 = [&](int kbuf) __attribute__((always_inline)) {
+        const uint16_t *kb0 = &Ks[kbuf][kfo];
+        constexpr int NKK = DP / 16, KA = 4;
+        bf16x8 ka[KA];
+#pragma unroll
+        for (int kk = 0; kk < KA - 1; ++kk)
+            ka[kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                s[rb][i] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            if (kk + KA - 1 < NKK)
+                ka[(kk + KA - 1) % KA] =
+                    as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + (kk + KA - 1) * KDK));
+            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk % KA], qb[0][kk], s[0], 0, 0, 0);
+            s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk % KA], qb[1][kk], s[1], 0, 0, 0);
+        }
+    };
+    // Keys at or past Sk (the last step only) take -inf.
+    auto mask = [&](int t) __attribute__((always_inline)) {
+        const int kbase = t * KT + kh * 32;
+        if (kbase + 32 > Sk) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (kbase + 16 * (i >> 3) + 8 * hi + (i & 7) >= Sk)
+                        s[rb][i] = kNegInf;
+        }
+    };
+    // The row max of the wave's 32 keys (both lane halves), one per row block.
+    auto rowmax = [&](int rb) -> float {
+        float m = max3f(s[rb][0], s[rb][1], s[rb][2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2)
+            m = max3f(m, s[rb][i], s[rb][i + 1]);
+        return max_xor32(fmaxf(m, s[rb][15]));
+    };
+    // p = 2^(s c - m c) of two scores: unit un of 16 (row block un / 8, scores (un % 8) * 2, +1),
+    // written as bf16 into the B operand half pk (written to LDS when its 8 values are in) and
+    // added as a pair to pr2 (pairwise tree per lane: pair, quad, octet, 16).
+    auto exp_unit = [&](int un, const float (&mc)[2], bf16x8 (&pk)[2], float (&pr2)[2][8])
+        __attribute__((always_inline)) {
+        const int rr = un / 8, i = (un % 8) * 2;
+        const float p0 = fast_exp2(fmaf(s[rr][i], c, -mc[rr]));
+        const float p1 = fast_exp2(fmaf(s[rr][i + 1], c, -mc[rr]));
+        pk[(i / 8) & 1][i % 8] = (__bf16)p0;
+        pk[(i / 8) & 1][i % 8 + 1] = (__bf16)p1;
+        pr2[rr][i / 2] = p0 + p1;
+    };
+    auto put_pk = [&](int pbuf, int rb, int hh, const bf16x8 &pk) {
+        *reinterpret_cast<u32x4 *>(&Ps[pbuf][w][(rb * 2 + hh) * PBLK + lane * 8]) =
+            __builtin_bit_cast(u32x4, pk);
+    };
+    auto sums = [&](const float (&pr2)[2][8], float (&ps)[2]) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            ps[rb] = ((pr2[rb][0] + pr2[rb][1]) + (pr2[rb][2] + pr2[rb][3])) +
+                     ((pr2[rb][4] + pr2[rb][5]) + (pr2[rb][6] + pr2[rb][7]));
+    };
+    auto mcs = [&](float (&mc)[2]) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            mc[rb] = (m_run[rb] == kNegInf) ? 0.f : m_run[rb] * c;
+    };
+    // The exponentials of the wave's scores into P (LDS buffer pbuf) and their per-lane sums.
+    auto exps = [&](int pbuf, float (&ps)[2]) __attribute__((always_inline)) {
+        float mc[2], pr2[2][8];
+        mcs(mc);
+        bf16x8 pk[2];
+#pragma unroll
+        for (int un = 0; un < 16; ++un) {
+            exp_unit(un, mc, pk, pr2);
+            if (un % 4 == 3)
+                put_pk(pbuf, un / 8, (un / 4) & 1, pk[(un / 4) & 1]);
+        }
+        sums(pr2, ps);
+    };
+    // O^T += V^T . P^T over the 64 keys of step tile (vbuf, pbuf) for the wave's d half, both
+    // P halves (its own and its partner's) read back from LDS, fused with exps of the next
+    // step's scores (EX: which do not depend on it) in a fixed order: each MFMA is followed by
+    // the exponentials of two scores per lane, so each wave overlaps its own VALU work with its
+    // MFMAs. Operands of 16-key step f (V fragments of both d blocks, P of both row blocks) are
+    // read two steps ahead.
+    auto pv_exps = [&](int vbuf, int pbuf, int pbuf_next, float (&ps)[2], auto ex)
+        __attribute__((always_inline)) {
+        constexpr bool EX = decltype(ex)::value;
+        const uint16_t *vb0 = &Vs[vbuf][vfo + kh * 2 * 128];
+        const uint16_t *pbw[2] = {&Ps[pbuf][kh ? w ^ 4 : w][lane * 8],
+                                  &Ps[pbuf][kh ? w : w ^ 4][lane * 8]}; // key halves 0, 1
+        float mc[2], pr2[2][8];
+        if constexpr (EX)
+            mcs(mc);
+        bf16x8 pk[2];
+        bf16x8 va[3][2], bp[3][2];
+        auto ld = [&](int f) { // operands of 16-key step f into ring slot f % 3
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                const uint16_t *vb = vb0 + f * 16 * DP + db * 128;
+                va[f % 3][db] = join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * DP));
+            }
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                bp[f % 3][rb] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                    pbw[f >> 1] + (rb * 2 + (f & 1)) * PBLK));
+        };
+        ld(0);
+        ld(1);
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<4>([&](auto F) __attribute__((always_inline)) {
+            constexpr int f = decltype(F)::value;
+            if constexpr (f + 2 < 4)
+                ld(f + 2);
+            static_for<4>([&](auto M) __attribute__((always_inline)) {
+                constexpr int db = decltype(M)::value / 2, rb = decltype(M)::value % 2;
+                constexpr int un = f * 4 + decltype(M)::value;
+                o[db][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[f % 3][db], bp[f % 3][rb],
+                                                                   o[db][rb], 0, 0, 0);
+                if constexpr (EX) {
+                    exp_unit(un, mc, pk, pr2);
+                    if constexpr (un % 4 == 3)
+                        put_pk(pbuf_next, un / 8, (un / 4) & 1, pk[(un / 4) & 1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+        if constexpr (EX)
+            sums(pr2, ps);
+    };
+    // Rare path for step tp, taken by every wave when any wave's p of that step failed the sum
+    // test (before P.V has used them): the scores are recomputed from the K tile still in LDS,
+    // the pair agrees the new row max, (l, o) are rescaled and the exponentials redone.
+    auto redo = [&](int tp) {
+        qk2(tp & 1);
+        mask(tp);
+        float mx[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            mx[rb] = rowmax(rb);
+            xm[w][rb * 64 + lane] = mx[rb];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const float mnew = fmaxf(m_run[rb], fmaxf(mx[rb], xm[w ^ 4][rb * 64 + lane]));
+            const float alpha = (mnew == m_run[rb]) ? 1.0f : fast_exp2((m_run[rb] - mnew) * c);
+            l_run[rb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+                o[db][rb] *= alpha;
+            m_run[rb] = mnew;
+        }
+        exps(tp & 1, ps_prev);
+        __syncthreads();
+    };
+
+    if (tid == 0) {
+        dflag[0] = -1;
+        dflag[1] = -1;
+    }
+    dma_k(0, 0);
+    dma_v(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): Q and this wave's blocks of step 0
+    __syncthreads();
+
+    // Step 0: the row max of both halves sets m.
+    if (nkt > 1) {
+        dma_k(1, 1);
+        dma_v(1, 1);
+    }
+    qk2(0);
+    mask(0);
+    {
+        float mx[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            mx[rb] = rowmax(rb);
+            xm[w][rb * 64 + lane] = mx[rb];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            m_run[rb] = fmaxf(mx[rb], xm[w ^ 4][rb * 64 + lane]);
+    }
+    exps(0, ps_prev);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+
+    // Step t: P.V of step t - 1 beside S^T and the exponentials of step t.
+    int vb = 0; // (t - 1) % 3
+    for (int t = 1; t < nkt; ++t) {
+        if (__builtin_amdgcn_readfirstlane(dflag[(t - 1) & 1]) == t)
+            redo(t - 1);
+        if (t + 1 < nkt) {
+            dma_k(t + 1, (t + 1) & 1);
+            dma_v(t + 1, vb == 0 ? 2 : vb - 1); // (t + 1) % 3
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            l_run[rb] += ps_prev[rb];
+        qk2(t & 1);
+        mask(t);
+        float ps[2];
+        pv_exps(vb, (t - 1) & 1, t & 1, ps, std::true_type{});
+        if (__builtin_amdgcn_ballot_w64(!(ps[0] <= kSumCap && ps[1] <= kSumCap)) != 0 && lane == 0)
+            dflag[t & 1] = t + 1;
+        ps_prev[0] = ps[0];
+        ps_prev[1] = ps[1];
+        vb = (vb == 2) ? 0 : vb + 1;
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    }
+    // The last step's P.V, then the pair's row sums and O.
+    if (__builtin_amdgcn_readfirstlane(dflag[(nkt - 1) & 1]) == nkt)
+        redo(nkt - 1);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+        l_run[rb] += ps_prev[rb];
+    {
+        float unused[2];
+        pv_exps(vb, (nkt - 1) & 1, 0, unused, std::false_type{});
+    }
+    float lt[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        lt[rb] = l_run[rb] + __shfl_xor(l_run[rb], 32);
+        xm[w][rb * 64 + lane] = lt[rb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        lt[rb] += xm[w ^ 4][rb * 64 + lane];
+        const int q = row0 + rb * 32 + l32;
+        if (q < Sq) {
+            const float inv = (lt[rb] > 0.f) ? 1.0f / lt[rb] : 0.f;
+            float *orow = O + ((size_t)h * Sq + q) * D;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const int d = kh * 64 + db * 32 + i4 * 8 + 4 * hi;
+                    f32x4 v = {o[db][rb][4 * i4] * inv, o[db][rb][4 * i4 + 1] * inv,
+                               o[db][rb][4 * i4 + 2] * inv, o[db][rb][4 * i4 + 3] * inv};
+                    if (d < D)
+                        *reinterpret_cast<f32x4 *>(orow + d) = v;
+                }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Decode (split-K). One workgroup per (kv head u, split sp, 16-row block rb) serves up to 16 of
 // the M = g*Sq <= 64 query rows of that kv head from one read of its K/V range
 // [sp*kps, min(sp*kps+kps, Sk)) (the row blocks of a range share it through L2). Waves
@@ -2255,6 +2632,29 @@ static int prefill_kt_forced() {
     return forced;
 }
 
+// The duo prefill (attn_prefill_duo_kernel) for 8-wave grids that fill the GPU: ATTN_PREFILL_DUO
+// =0 or =1 (read once) turns it off or on for tuning sweeps.
+static int prefill_duo() {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_DUO");
+        env = (e && (atoi(e) == 1 || atoi(e) == 2)) ? atoi(e) : 0;
+    }
+    return env;
+}
+
+template <int DP>
+hipError_t launch_prefill_duo(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
+                              int Hq, int Hkv, int Sq, int Sk, int D, float c, hipStream_t st) {
+    const int nqt = (Sq + 255) / 256;
+    const long nblk = (long)Hq * nqt;
+    if (nblk <= 0 || nblk > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((attn_prefill_duo_kernel<DP>), dim3((unsigned)nblk), dim3(512), 0, st, Q, K,
+                       V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nblk);
+    return hipGetLastError();
+}
+
 template <int DP, int KT, bool CAUSAL, bool VT>
 hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                                  int Hq, int Hkv, int Sq, int Sk, int D, float c, float *pm,
@@ -2279,6 +2679,11 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
+    if constexpr (DP == 128 && KT == 128 && !CAUSAL && !VT)
+        if (!prefill_pack(Hq, Hkv, Sq) &&
+            ((nw == 8 && prefill_duo() == 1 && 2L * Hq * ((Sq + 255) / 256) > device_cus()) ||
+             prefill_duo() == 2))
+            return launch_prefill_duo<DP>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
