@@ -72,10 +72,11 @@ def test_lds_dma_kernels_have_no_compiler_dma_waits(funcs):
 def test_kernels_make_only_the_deliberate_library_call(funcs):
     """HIP's id builtins are out-of-line calls in this build; the kernels read the ids directly,
     except one threadIdx.x in each LDS-DMA kernel (the call that keeps the loop above free of
-    compiler DMA waits)."""
+    compiler DMA waits): the fast and persistent prefills and the V^T decode."""
     for name, ins in funcs.items():
         if not name.startswith("_Z") or "attn_" not in name:
             continue
         calls = sum(1 for x in ins if x.startswith("s_swappc"))
-        want = 1 if ("attn_prefill_fast_kernel" in name or "attn_decode_vt_kernel" in name) else 0
+        want = 1 if any(k in name for k in ("attn_prefill_fast_kernel", "attn_prefill_persist_kernel",
+                                            "attn_decode_vt_kernel")) else 0
         assert calls == want, (name, calls)

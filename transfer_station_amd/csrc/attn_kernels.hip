@@ -1251,379 +1251,399 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill, duo layout (non-causal, row-major V, 64 < D <= DP = 128, full grids). In the fast
-// kernel each wave owns 32 query rows, so every K or V fragment read from LDS (1 KB) feeds one
-// MFMA; with all 8 waves of a CU reading their fragments, the LDS, not the MFMA pipe, bounds a
-// key tile. Here the 8 waves of a workgroup serve its 256 rows as 4 pairs: waves w and w + 4
-// share the 64 rows pr*64 .. (pr = w % 4) and split the work of every 64-key step:
-//   S^T = K . Q^T    wave half kh = w / 4 takes the step's keys kh*32 .. +31 for all 64 rows:
-//                    each K fragment feeds two MFMAs (one per 32-row block);
-//   softmax          p = 2^(s c - m c) for those 64 x 32 scores, P (bf16) written to LDS;
-//   O^T += V^T.P^T   one step later (software-pipelined), each wave accumulates the 64 d columns
-//                    dh = kh of its half over all 64 keys of the step: its own P from registers,
-//                    the partner's from LDS; each V fragment feeds two MFMAs.
-// Per wave and step: 32 MFMA and 24 KB of LDS traffic (K 8, V 8, P 4 written + 4 read), against
-// 32 MFMA and 32 KB in the fast kernel. LDS: K x 2, V x 3 and P x 2 step buffers (148 KB); one
-// barrier per step publishes the next step's K/V (issued at the start of the step) and this
-// step's P. The two waves of a pair keep one running max m per row: it is set from both halves
-// on the first step; later steps test each lane's sum of p against kSumCap, and a failing wave
-// raises a workgroup flag, on which every wave recomputes that step's scores, agrees a new max
-// with its partner and redoes its exponentials before P.V consumes them. l sums each wave's own
-// keys; the pair adds its two sums at the end.
+// Prefill, persistent (non-causal, D % 8 == 0, D <= DP = 128, at least two rounds of 8-wave
+// workgroups). The fast kernel runs one (query head, 256-row tile) item per workgroup, and each
+// item pays a fixed cost outside its key loop: all CUs load Q and the first key tile at once
+// (an HBM burst), store O at once, and wait for the next workgroup's dispatch. Here one 8-wave
+// workgroup per CU runs its items back to back, and the key-tile pipeline continues across
+// them:
+//   * the next item's first K/V tile is the last tile's ordinary LDS-DMA prefetch;
+//   * the next item's Q (registers) is loaded during the last tile, after its S^T, so it lands
+//     under the softmax and P.V (the last tile takes the row max, so no recompute needs the
+//     old Q);
+//   * an item's O leaves as 16 buffer stores per lane (rows past Sq fall outside the
+//     descriptor's range: the count never depends on the data), issued in the next item's first
+//     tile after that tile's DMA; the wait for the DMA then leaves exactly those 16 stores in
+//     flight (vmcnt(16): vector memory operations complete in issue order), so the O write
+//     burst drains under the next tile's compute.
+// Items of a CU follow the non-persistent grid's rounds: XCD x = b % 8 holds the logical items
+// [xb, xb + nx) (kv-head-major, as xcd_remap deals them) and its i-th workgroup takes
+// xb + i, xb + i + R, ... (R workgroups per XCD), so each round of an XCD shares one kv head's
+// K/V in its L2 as before. The tile code is the fast kernel's (8 waves, 32 rows each, 128-key
+// tiles, lazy rescale with the sum test), without causal masks, for row-major V only: a V^T
+// variant needs 4 more offset registers for its DMA, spills them, and its spill reloads then
+// wait for the DMA in flight (measured 0.5-2.6% slower than the V^T fast kernel on c3 and c4).
 // ------------------------------------------------------------------------------------------
+// s_waitcnt operand (gfx9 encoding) that waits until at most n vector memory operations of
+// the wave are in flight, with no wait on expcnt or lgkmcnt.
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 template <int DP>
-__global__ __launch_bounds__(512, 1) void attn_prefill_duo_kernel(
+__global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
-    float c, int nqt, int nwg) {
-    static_assert(DP == 128, "two 64-column halves of D");
-    constexpr int KT = 64;  // keys per step
-    constexpr int NW = 8;   // waves
-    constexpr int BQ = 256; // query rows per workgroup
-    constexpr int NI = KT * DP / 512; // 1 KB DMA blocks per tensor and step
-    constexpr int PW = NI / NW;
-    static_assert(PW * NW == NI, "DMA blocks per wave");
-    constexpr int KSUB = 32 * DP, KDK = 128; // K fragment steps (elements): 32 keys, 16 d
-    constexpr int PBLK = 64 * 8;             // one B operand (64 lanes x 8 bf16) of P
-    __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
-    __shared__ __attribute__((aligned(1024))) uint16_t Vs[3][KT * DP];
-    __shared__ __attribute__((aligned(1024))) uint16_t Ps[2][NW][4 * PBLK];
-    __shared__ float xm[NW][128]; // row maxima, and at the end row sums, for the partner
-    __shared__ int dflag[2];      // step t + 1 when a wave's p of step t failed the sum test
+    float c, int nqt, int nitems, int nwg) {
+    static_assert(DP % 32 == 0 && DP <= 128, "tile shape");
+    constexpr int KT = 128, NW = 8, BQ = NW * 32;
+    // One variable per tile buffer: the compiler tells LDS accesses apart by variable only, so
+    // with the two buffers of an array it would make each tile's first reads wait for the DMA
+    // of the next tile into the other buffer.
+    __shared__ __attribute__((aligned(1024))) uint16_t Ks0[KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Ks1[KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs0[KT * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t Vs1[KT * DP];
+    auto kbuf = [&](int buf) -> uint16_t * { return buf ? Ks1 : Ks0; }; // buf: a constant
+    auto vbuf = [&](int buf) -> uint16_t * { return buf ? Vs1 : Vs0; };
 
     const int g = Hq / Hkv;
-    const int L = xcd_remap(wg_id_x(), nwg);
-    const int uu = L / (g * nqt);
-    const int rr = L - uu * (g * nqt);
-    const int qt = rr / g;
-    const int h = uu * g + (rr - qt * g);
-    const int u = __builtin_amdgcn_readfirstlane(h / g); // kv head
+    const int b = wg_id_x(), x = b & 7, xi = b >> 3, R = nwg >> 3; // nwg % 8 == 0
+    const int per = nitems >> 3, rem = nitems & 7;
+    const int xb = (x < rem) ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+    const int nx = per + (x < rem ? 1 : 0);
+    const int nmine = (xi < nx) ? (nx - xi + R - 1) / R : 0;
+    if (nmine == 0)
+        return;
+    // Item k of this workgroup: query head h and 256-row tile qt (the fast kernel's non-causal
+    // order: kv head, then tile, then the g heads of the group).
+    auto item = [&](int k, int &h, int &qt) {
+        const int L = xb + xi + k * R;
+        const int uu = L / (g * nqt);
+        const int rr = L - uu * (g * nqt);
+        qt = __builtin_amdgcn_readfirstlane(rr / g);
+        h = __builtin_amdgcn_readfirstlane(uu * g + (rr - (rr / g) * g));
+    };
 
     const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pr = w & 3, kh = w >> 2; // row block pair, key half (and d half) of the wave
+    // & 7: the compiler then knows each wave's DMA blocks stay inside one tile buffer
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & 7;
     const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
-    const int row0 = qt * BQ + pr * 64; // the pair's first row
+    const int nkt = (Sk + KT - 1) / KT; // even (host)
 
-    bf16x8 qb[2][DP / 16];
+    const uint32_t qbytes = (uint32_t)Sq * (uint32_t)D * 2u; // one head of Q (O: twice; < 2^31)
+    // Q rows of item (h, qt) for this lane's operand layout: 16-byte buffer loads, rows past Sq
+    // and columns past D outside the descriptor's range (zeros), DP/16 loads whatever the data.
+    bf16x8 qb[DP / 16];
+    auto load_q = [&](int h, int qt) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q + (size_t)h * Sq * D, qbytes);
+        // r is made opaque here (and in store_o, and kbase in the last tile's mask): the
+        // offsets and key compares are the same for every item, and hoisted out of the item
+        // loop they would hold their registers (64 lane masks, 24 offsets) for the whole kernel.
+        int r = w * 32 + l32;
+        asm volatile("" : "+v"(r));
+        r += qt * BQ; // row of the head
+        const int dlim = (r < Sq) ? D : 0;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        const int q = row0 + rb * 32 + l32;
-#pragma unroll
-        for (int kk = 0; kk < DP / 16; ++kk)
-            qb[rb][kk] = as_bf16x8(load_row8<true>(Q, (size_t)h * Sq + (size_t)(q < Sq ? q : 0),
-                                                   kk * 16 + hi * 8, D, q < Sq));
-    }
+        for (int kk = 0; kk < DP / 16; ++kk) {
+            const int col = kk * 16 + hi * 8;
+            const uint32_t off = (col < dlim) ? (uint32_t)(r * D + col) * 2u : 0x80000000u;
+            qb[kk] = as_bf16x8(__builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, 0)));
+        }
+    };
 
-    // DMA source offsets of this wave's blocks of a K or V step tile (layouts as in
-    // attn_prefill_fast_kernel; a chunk of columns D and beyond arrives as zero).
+    // LDS-DMA source offsets of this wave's blocks (layouts as in attn_prefill_fast_kernel).
+    constexpr int NI = KT * DP / 512;
+    constexpr int PW = NI / NW;
+    static_assert(PW * NW == NI && PW >= 1, "DMA blocks per wave");
     const uint32_t kvbytes = (uint32_t)Sk * D * 2;
     uint32_t kso[PW], vso[PW];
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
-        const int b = (w * PW + k) * 1024 + 16 * lane;
+        const int bb = (w * PW + k) * 1024 + 16 * lane;
         {
-            const int rg = b / (16 * DP), wi = b % (16 * DP);
+            const int rg = bb / (16 * DP), wi = bb % (16 * DP);
             const int r = rg * 8 + (wi % 256) / 32;
             const int cc = 2 * (wi / 256) + (((wi % 32) / 16) ^ (rg & 1));
             kso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
         }
         {
-            const int rgv = b / (8 * DP), wi = b % (8 * DP);
+            const int rgv = bb / (8 * DP), wi = bb % (8 * DP);
             const int r = rgv * 4 + (wi % 256) / 64;
             const int cc = 4 * (wi / 256) + (wi % 64) / 16;
             vso[k] = (cc * 8 < D) ? (uint32_t)(r * D * 2 + cc * 16) : 0x80000000u;
         }
     }
-    auto dma_k = [&](int kt, int buf) {
+    // K and V tile kt of kv head u into LDS buffer buf: 2 * PW DMA instructions.
+    auto dma_kv = [&](int u, int kt, int buf) __attribute__((always_inline)) {
         const uint32_t toff = (uint32_t)kt * KT * D * 2;
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(K + (size_t)u * Sk * D + (size_t)kt * KT * D,
-                                                   kvbytes - toff);
+        const __amdgpu_buffer_rsrc_t rk =
+            make_rsrc(K + (size_t)u * Sk * D + (size_t)kt * KT * D, kvbytes - toff);
+        const __amdgpu_buffer_rsrc_t rv =
+            make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D, kvbytes - toff);
 #pragma unroll
         for (int k = 0; k < PW; ++k)
-            dma16<0>(r, &Ks[buf][(w * PW + k) * 512], kso[k]);
-    };
-    auto dma_v = [&](int kt, int buf) {
-        const uint32_t toff = (uint32_t)kt * KT * D * 2;
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(V + (size_t)u * Sk * D + (size_t)kt * KT * D,
-                                                   kvbytes - toff);
+            dma16<0>(rk, &kbuf(buf)[(w * PW + k) * 512], kso[k]);
 #pragma unroll
         for (int k = 0; k < PW; ++k)
-            dma16<0>(r, &Vs[buf][(w * PW + k) * 512], vso[k]);
+            dma16<0>(rv, &vbuf(buf)[(w * PW + k) * 512], vso[k]);
     };
+    constexpr int NOST = DP / 8; // vector memory instructions of one store_o
 
-    // Fragment offsets (elements), as in attn_prefill_fast_kernel: K row kh*32 + kperm, chunk
-    // 2kk + hi; V rows cc*16 + 8hi + i16/4 (+4), columns db*32 + (g16&1)*16 + 4(i16&3).
     const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
-    const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8) +
-                    kh * KSUB;
-    const int vfo = hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
-                    (i16 & 1) * 4;
+    const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
+    constexpr int KSUB = 32 * DP, KDK = 128;
+    const int vfo =
+        hi * 8 * DP + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 + (i16 & 1) * 4;
 
-    const int nkt = (Sk + KT - 1) / KT;
-    float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f}, ps_prev[2] = {0.f, 0.f};
-    f32x16 o[2][2]; // [d block of the wave's half][row block]
+    float m_run = kNegInf, l_run = 0.f;
+    f32x16 o[DP / 32];
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < DP / 32; ++db)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int i = 0; i < 16; ++i)
+            o[db][i] = 0.f;
+    f32x16 s[KT / 32];
+    bf16x8 pk[KT / 16];
+    bf16x8 va[2][DP / 32];
+
+    // S^T = K_tile . Q^T (the next sub-tile's K fragments read between this one's MFMAs).
+    auto qk = [&](int buf) __attribute__((always_inline)) {
+        const uint16_t *kb0 = &kbuf(buf)[kfo];
+        bf16x8 ka[2][DP / 16];
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+            ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
+        __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t) {
 #pragma unroll
             for (int i = 0; i < 16; ++i)
-                o[db][rb][i] = 0.f;
-    f32x16 s[2];
-
-    // S^T for the wave's 32 keys of step tile kbuf and both row blocks; K fragments are read
-    // KA - 1 16-d steps ahead (each feeds two MFMAs).
-    auto qk2 = [&](int kbuf) __attribute__((always_inline)) {
-        const uint16_t *kb0 = &Ks[kbuf][kfo];
-        constexpr int NKK = DP / 16, KA = 4;
-        bf16x8 ka[KA];
+                s[t][i] = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < KA - 1; ++kk)
-            ka[kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                s[rb][i] = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-            if (kk + KA - 1 < NKK)
-                ka[(kk + KA - 1) % KA] =
-                    as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + (kk + KA - 1) * KDK));
-            s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk % KA], qb[0][kk], s[0], 0, 0, 0);
-            s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[kk % KA], qb[1][kk], s[1], 0, 0, 0);
-        }
-    };
-    // Keys at or past Sk (the last step only) take -inf.
-    auto mask = [&](int t) __attribute__((always_inline)) {
-        const int kbase = t * KT + kh * 32;
-        if (kbase + 32 > Sk) {
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (kbase + 16 * (i >> 3) + 8 * hi + (i & 7) >= Sk)
-                        s[rb][i] = kNegInf;
-        }
-    };
-    // The row max of the wave's 32 keys (both lane halves), one per row block.
-    auto rowmax = [&](int rb) -> float {
-        float m = max3f(s[rb][0], s[rb][1], s[rb][2]);
-#pragma unroll
-        for (int i = 3; i < 15; i += 2)
-            m = max3f(m, s[rb][i], s[rb][i + 1]);
-        return max_xor32(fmaxf(m, s[rb][15]));
-    };
-    // p = 2^(s c - m c) of two scores: unit un of 16 (row block un / 8, scores (un % 8) * 2, +1),
-    // written as bf16 into the B operand half pk (written to LDS when its 8 values are in) and
-    // added as a pair to pr2 (pairwise tree per lane: pair, quad, octet, 16).
-    auto exp_unit = [&](int un, const float (&mc)[2], bf16x8 (&pk)[2], float (&pr2)[2][8])
-        __attribute__((always_inline)) {
-        const int rr = un / 8, i = (un % 8) * 2;
-        const float p0 = fast_exp2(fmaf(s[rr][i], c, -mc[rr]));
-        const float p1 = fast_exp2(fmaf(s[rr][i + 1], c, -mc[rr]));
-        pk[(i / 8) & 1][i % 8] = (__bf16)p0;
-        pk[(i / 8) & 1][i % 8 + 1] = (__bf16)p1;
-        pr2[rr][i / 2] = p0 + p1;
-    };
-    auto put_pk = [&](int pbuf, int rb, int hh, const bf16x8 &pk) {
-        *reinterpret_cast<u32x4 *>(&Ps[pbuf][w][(rb * 2 + hh) * PBLK + lane * 8]) =
-            __builtin_bit_cast(u32x4, pk);
-    };
-    auto sums = [&](const float (&pr2)[2][8], float (&ps)[2]) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            ps[rb] = ((pr2[rb][0] + pr2[rb][1]) + (pr2[rb][2] + pr2[rb][3])) +
-                     ((pr2[rb][4] + pr2[rb][5]) + (pr2[rb][6] + pr2[rb][7]));
-    };
-    auto mcs = [&](float (&mc)[2]) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            mc[rb] = (m_run[rb] == kNegInf) ? 0.f : m_run[rb] * c;
-    };
-    // The exponentials of the wave's scores into P (LDS buffer pbuf) and their per-lane sums.
-    auto exps = [&](int pbuf, float (&ps)[2]) __attribute__((always_inline)) {
-        float mc[2], pr2[2][8];
-        mcs(mc);
-        bf16x8 pk[2];
-#pragma unroll
-        for (int un = 0; un < 16; ++un) {
-            exp_unit(un, mc, pk, pr2);
-            if (un % 4 == 3)
-                put_pk(pbuf, un / 8, (un / 4) & 1, pk[(un / 4) & 1]);
-        }
-        sums(pr2, ps);
-    };
-    // O^T += V^T . P^T over the 64 keys of step tile (vbuf, pbuf) for the wave's d half, both
-    // P halves (its own and its partner's) read back from LDS, fused with exps of the next
-    // step's scores (EX: which do not depend on it) in a fixed order: each MFMA is followed by
-    // the exponentials of two scores per lane, so each wave overlaps its own VALU work with its
-    // MFMAs. Operands of 16-key step f (V fragments of both d blocks, P of both row blocks) are
-    // read two steps ahead.
-    auto pv_exps = [&](int vbuf, int pbuf, int pbuf_next, float (&ps)[2], auto ex)
-        __attribute__((always_inline)) {
-        constexpr bool EX = decltype(ex)::value;
-        const uint16_t *vb0 = &Vs[vbuf][vfo + kh * 2 * 128];
-        const uint16_t *pbw[2] = {&Ps[pbuf][kh ? w ^ 4 : w][lane * 8],
-                                  &Ps[pbuf][kh ? w : w ^ 4][lane * 8]}; // key halves 0, 1
-        float mc[2], pr2[2][8];
-        if constexpr (EX)
-            mcs(mc);
-        bf16x8 pk[2];
-        bf16x8 va[3][2], bp[3][2];
-        auto ld = [&](int f) { // operands of 16-key step f into ring slot f % 3
-#pragma unroll
-            for (int db = 0; db < 2; ++db) {
-                const uint16_t *vb = vb0 + f * 16 * DP + db * 128;
-                va[f % 3][db] = join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * DP));
+            for (int kk = 0; kk < DP / 16; ++kk) {
+                s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
+                if (t + 1 < KT / 32)
+                    ka[(t + 1) & 1][kk] = as_bf16x8(
+                        *reinterpret_cast<const u32x4 *>(kb0 + (t + 1) * KSUB + kk * KDK));
             }
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-                bp[f % 3][rb] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
-                    pbw[f >> 1] + (rb * 2 + (f & 1)) * PBLK));
-        };
-        ld(0);
-        ld(1);
+            for (int kk = 0; kk < DP / 16; ++kk) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (t + 1 < KT / 32)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+    };
+    // Keys at or past Sk (an item's last tile only) take -inf: sub-tiles wholly before Sk are
+    // skipped and sub-tiles wholly past it set at once (wave-uniform tests), so only the
+    // sub-tile that Sk crosses is compared key by key.
+    auto mask = [&](int kbase) __attribute__((always_inline)) {
+        if (kbase + KT > Sk) {
+#pragma unroll
+            for (int t = 0; t < KT / 32; ++t) {
+                const int k0t = kbase + t * 32;
+                if (k0t + 32 <= Sk)
+                    continue;
+                if (k0t >= Sk) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        s[t][i] = kNegInf;
+                    continue;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (k0t + 16 * (i >> 3) + 8 * hi + (i & 7) >= Sk)
+                        s[t][i] = kNegInf;
+            }
+        }
+    };
+    auto row_max = [&]() __attribute__((always_inline)) {
+        float mt[KT / 32];
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t) {
+            float m = max3f(s[t][0], s[t][1], s[t][2]);
+#pragma unroll
+            for (int i = 3; i < 15; i += 2)
+                m = max3f(m, s[t][i], s[t][i + 1]);
+            mt[t] = fmaxf(m, s[t][15]);
+        }
+        const float mx = max_xor32(fmaxf(max3f(mt[0], mt[1], mt[2]), mt[3]));
+        const bool raise = mx > m_run;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+            const float mnew = raise ? mx : m_run;
+            const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+                o[db] *= alpha;
+            m_run = mnew;
+        }
+    };
+    auto exps = [&]() __attribute__((always_inline)) -> float {
+        const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
+        float ps[KT / 16];
+#pragma unroll
+        for (int t = 0; t < KT / 32; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float p[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    p[j] = fast_exp2(fmaf(s[t][8 * hh + j], c, -mc));
+                    pk[2 * t + hh][j] = (__bf16)p[j];
+                }
+                ps[2 * t + hh] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+            }
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < KT / 16; ++j)
+            psum += ps[j];
+        return psum;
+    };
+    auto vfrag = [&](int buf, int cc, int db) -> bf16x8 {
+        const uint16_t *vb = &vbuf(buf)[vfo + cc * 16 * DP + db * 128];
+        return join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * DP));
+    };
+    auto pv_first = [&](int buf) {
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+            va[0][db] = vfrag(buf, 0, db);
+    };
+    auto pv = [&](int buf) {
+#pragma unroll
+        for (int cc = 0; cc < KT / 16; ++cc) {
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db) {
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], o[db], 0, 0,
+                                                               0);
+                if (cc + 1 < KT / 16)
+                    va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
+            }
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (cc + 1 < KT / 16)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+        }
+    };
+    // O of item (h, qt) from (o, l): NOST buffer stores whatever the data (none lands when
+    // !valid: every offset is then outside the descriptor's range).
+    auto store_o = [&](int h, int qt, bool valid) __attribute__((always_inline)) {
+        const float lt = l_run + __shfl_xor(l_run, 32);
+        const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
+        const __amdgpu_buffer_rsrc_t ro = make_rsrc(O + (size_t)h * Sq * D, 2u * qbytes);
+        int r = w * 32 + l32;
+        asm volatile("" : "+v"(r));
+        r += qt * BQ; // row of the head
+        // One column limit per lane (D, or 0 for a row to drop): a single compare per store
+        // keeps the stores free of branches.
+        const int dlim = (valid & (r < Sq)) ? D : 0;
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int d = db * 32 + i4 * 8 + 4 * hi;
+                const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv,
+                                 o[db][4 * i4 + 2] * inv, o[db][4 * i4 + 3] * inv};
+                const uint32_t off = (d < dlim) ? (uint32_t)(r * D + d) * 4u : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0, 0);
+            }
+    };
+
+    {
+        int h0, qt0;
+        item(0, h0, qt0);
+        load_q(h0, qt0);
+        dma_kv(__builtin_amdgcn_readfirstlane(h0 / g), 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): Q and tile 0 of the first item
+    __syncthreads();
+    // One key tile of item k (kv head u): FIRST (kt = 0: the previous item's O leaves, then the
+    // row max), LAST (kt = nkt - 1: the next item's tile 0 DMA and Q loads, the Sk mask, the row
+    // max) or neither (the sum test, a rare recompute). Item coordinates are recomputed from
+    // the item index where needed rather than carried in registers.
+    // nkt is even (host), so tile kt of every item uses LDS buffer kt & 1: each step's buffers
+    // are constants, which lets the compiler tell this tile's LDS reads from the next tile's DMA
+    // (with a run-time buffer index it waits for that DMA before the first read).
+    auto step = [&](int u, int kt, int k, auto kbuf, auto kfirst, auto klast)
+        __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(kfirst)::value, LAST = decltype(klast)::value;
+        constexpr int buf = decltype(kbuf)::value;
+        const bool more = k + 1 < nmine;
+        // The next tile's DMA, the oldest vector memory operation of the tile.
+        if (!LAST) {
+            dma_kv(u, kt + 1, buf ^ 1);
+        } else if (more) {
+            int hn, qtn;
+            item(k + 1, hn, qtn);
+            dma_kv(__builtin_amdgcn_readfirstlane(hn / g), 0, buf ^ 1);
+        }
+        if (FIRST) {
+            // The previous item's O (after this tile's DMA; for the first item the stores are
+            // issued but land nowhere, which keeps this tile free of branches), then a fresh
+            // state.
+            int hp, qtp;
+            item(k > 0 ? k - 1 : 0, hp, qtp);
+            store_o(hp, qtp, k > 0);
+            m_run = kNegInf;
+            l_run = 0.f;
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    o[db][i] = 0.f;
+        }
+        qk(buf);
+        pv_first(buf);
+        // The fast kernel's phase order: S^T, then the softmax, then P.V (letting the compiler
+        // move the first sub-tile's exponentials between the later sub-tiles' MFMAs measured
+        // slower: in-wave VALU between MFMAs delays the wave's own S^T).
         __builtin_amdgcn_sched_barrier(0);
-        static_for<4>([&](auto F) __attribute__((always_inline)) {
-            constexpr int f = decltype(F)::value;
-            if constexpr (f + 2 < 4)
-                ld(f + 2);
-            static_for<4>([&](auto M) __attribute__((always_inline)) {
-                constexpr int db = decltype(M)::value / 2, rb = decltype(M)::value % 2;
-                constexpr int un = f * 4 + decltype(M)::value;
-                o[db][rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[f % 3][db], bp[f % 3][rb],
-                                                                   o[db][rb], 0, 0, 0);
-                if constexpr (EX) {
-                    exp_unit(un, mc, pk, pr2);
-                    if constexpr (un % 4 == 3)
-                        put_pk(pbuf_next, un / 8, (un / 4) & 1, pk[(un / 4) & 1]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            });
-        });
-        if constexpr (EX)
-            sums(pr2, ps);
+        if (LAST && more) { // qb is free: this tile takes the row max, with no recompute
+            int hn, qtn;
+            item(k + 1, hn, qtn);
+            load_q(hn, qtn);
+        }
+        if (FIRST || LAST) {
+            if (LAST) {
+                int kbase = kt * KT;
+                asm volatile("" : "+s"(kbase));
+                mask(kbase);
+            }
+            row_max();
+            l_run += exps();
+        } else {
+            float psum = exps();
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(psum <= kSumCap)) != 0, 0)) {
+                qk(buf);
+                pv_first(buf);
+                row_max();
+                psum = exps();
+            }
+            l_run += psum;
+        }
+        pv(buf);
+        if (!LAST || more) {
+            // Wait for the next tile's DMA only: the O stores of tile 0 (NOST) are younger and
+            // stay in flight. The last tile waits for everything (the next item's Q loads, issued
+            // mid-tile, have landed by then), so each item starts with no vector memory operation
+            // in flight: with one still pending at the item loop's head the compiler waits for it
+            // before the first tile's LDS reads.
+            if (FIRST)
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(NOST));
+            else
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
     };
-    // Rare path for step tp, taken by every wave when any wave's p of that step failed the sum
-    // test (before P.V has used them): the scores are recomputed from the K tile still in LDS,
-    // the pair agrees the new row max, (l, o) are rescaled and the exponentials redone.
-    auto redo = [&](int tp) {
-        qk2(tp & 1);
-        mask(tp);
-        float mx[2];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            mx[rb] = rowmax(rb);
-            xm[w][rb * 64 + lane] = mx[rb];
+    for (int k = 0; k < nmine; ++k) {
+        int h, qt;
+        item(k, h, qt);
+        const int u = __builtin_amdgcn_readfirstlane(h / g);
+        using B0 = std::integral_constant<int, 0>;
+        using B1 = std::integral_constant<int, 1>;
+        step(u, 0, k, B0{}, std::true_type{}, std::false_type{});
+        for (int kt = 1; kt + 1 < nkt; kt += 2) {
+            step(u, kt, k, B1{}, std::false_type{}, std::false_type{});
+            step(u, kt + 1, k, B0{}, std::false_type{}, std::false_type{});
         }
-        __syncthreads();
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const float mnew = fmaxf(m_run[rb], fmaxf(mx[rb], xm[w ^ 4][rb * 64 + lane]));
-            const float alpha = (mnew == m_run[rb]) ? 1.0f : fast_exp2((m_run[rb] - mnew) * c);
-            l_run[rb] *= alpha;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-                o[db][rb] *= alpha;
-            m_run[rb] = mnew;
-        }
-        exps(tp & 1, ps_prev);
-        __syncthreads();
-    };
-
-    if (tid == 0) {
-        dflag[0] = -1;
-        dflag[1] = -1;
+        step(u, nkt - 1, k, B1{}, std::false_type{}, std::true_type{});
     }
-    dma_k(0, 0);
-    dma_v(0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): Q and this wave's blocks of step 0
-    __syncthreads();
-
-    // Step 0: the row max of both halves sets m.
-    if (nkt > 1) {
-        dma_k(1, 1);
-        dma_v(1, 1);
-    }
-    qk2(0);
-    mask(0);
     {
-        float mx[2];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            mx[rb] = rowmax(rb);
-            xm[w][rb * 64 + lane] = mx[rb];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            m_run[rb] = fmaxf(mx[rb], xm[w ^ 4][rb * 64 + lane]);
-    }
-    exps(0, ps_prev);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-
-    // Step t: P.V of step t - 1 beside S^T and the exponentials of step t.
-    int vb = 0; // (t - 1) % 3
-    for (int t = 1; t < nkt; ++t) {
-        if (__builtin_amdgcn_readfirstlane(dflag[(t - 1) & 1]) == t)
-            redo(t - 1);
-        if (t + 1 < nkt) {
-            dma_k(t + 1, (t + 1) & 1);
-            dma_v(t + 1, vb == 0 ? 2 : vb - 1); // (t + 1) % 3
-        }
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            l_run[rb] += ps_prev[rb];
-        qk2(t & 1);
-        mask(t);
-        float ps[2];
-        pv_exps(vb, (t - 1) & 1, t & 1, ps, std::true_type{});
-        if (__builtin_amdgcn_ballot_w64(!(ps[0] <= kSumCap && ps[1] <= kSumCap)) != 0 && lane == 0)
-            dflag[t & 1] = t + 1;
-        ps_prev[0] = ps[0];
-        ps_prev[1] = ps[1];
-        vb = (vb == 2) ? 0 : vb + 1;
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
-    }
-    // The last step's P.V, then the pair's row sums and O.
-    if (__builtin_amdgcn_readfirstlane(dflag[(nkt - 1) & 1]) == nkt)
-        redo(nkt - 1);
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-        l_run[rb] += ps_prev[rb];
-    {
-        float unused[2];
-        pv_exps(vb, (nkt - 1) & 1, 0, unused, std::false_type{});
-    }
-    float lt[2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        lt[rb] = l_run[rb] + __shfl_xor(l_run[rb], 32);
-        xm[w][rb * 64 + lane] = lt[rb];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-        lt[rb] += xm[w ^ 4][rb * 64 + lane];
-        const int q = row0 + rb * 32 + l32;
-        if (q < Sq) {
-            const float inv = (lt[rb] > 0.f) ? 1.0f / lt[rb] : 0.f;
-            float *orow = O + ((size_t)h * Sq + q) * D;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int i4 = 0; i4 < 4; ++i4) {
-                    const int d = kh * 64 + db * 32 + i4 * 8 + 4 * hi;
-                    f32x4 v = {o[db][rb][4 * i4] * inv, o[db][rb][4 * i4 + 1] * inv,
-                               o[db][rb][4 * i4 + 2] * inv, o[db][rb][4 * i4 + 3] * inv};
-                    if (d < D)
-                        *reinterpret_cast<f32x4 *>(orow + d) = v;
-                }
-        }
+        int hl, qtl;
+        item(nmine - 1, hl, qtl);
+        store_o(hl, qtl, true);
     }
 }
 
@@ -2632,26 +2652,30 @@ static int prefill_kt_forced() {
     return forced;
 }
 
-// The duo prefill (attn_prefill_duo_kernel) for 8-wave grids that fill the GPU: ATTN_PREFILL_DUO
-// =0 or =1 (read once) turns it off or on for tuning sweeps.
-static int prefill_duo() {
+// The persistent prefill (attn_prefill_persist_kernel) for non-causal 8-wave grids of at least
+// two rounds: ATTN_PREFILL_PERSIST=0 (read once) turns it off for tuning sweeps.
+static int prefill_persist() {
     static int env = -1;
     if (env < 0) {
-        const char *e = getenv("ATTN_PREFILL_DUO");
-        env = (e && (atoi(e) == 1 || atoi(e) == 2)) ? atoi(e) : 0;
+        const char *e = getenv("ATTN_PREFILL_PERSIST");
+        env = (e && atoi(e) == 0) ? 0 : 1;
     }
     return env;
 }
 
+// One workgroup per CU (a multiple of 8: each XCD takes the same count), each running its
+// items of the 256-row tiling back to back.
 template <int DP>
-hipError_t launch_prefill_duo(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
-                              int Hq, int Hkv, int Sq, int Sk, int D, float c, hipStream_t st) {
+hipError_t launch_prefill_persist(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
+                                  float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
+                                  hipStream_t st) {
     const int nqt = (Sq + 255) / 256;
-    const long nblk = (long)Hq * nqt;
-    if (nblk <= 0 || nblk > 0x7fffffffL)
+    const long nitems = (long)Hq * nqt;
+    const int nwg = device_cus() / 8 * 8;
+    if (nitems <= 0 || nitems > 0x7fffffffL || nwg <= 0)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_duo_kernel<DP>), dim3((unsigned)nblk), dim3(512), 0, st, Q, K,
-                       V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nblk);
+    hipLaunchKernelGGL((attn_prefill_persist_kernel<DP>), dim3((unsigned)nwg), dim3(512), 0, st,
+                       Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nitems, nwg);
     return hipGetLastError();
 }
 
@@ -2679,11 +2703,13 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
+    // Grids of at least two rounds of 8-wave workgroups with an even number (at least two) of
+    // key tiles per item and row-major V run persistent (attn_prefill_persist_kernel).
     if constexpr (DP == 128 && KT == 128 && !CAUSAL && !VT)
-        if (!prefill_pack(Hq, Hkv, Sq) &&
-            ((nw == 8 && prefill_duo() == 1 && 2L * Hq * ((Sq + 255) / 256) > device_cus()) ||
-             prefill_duo() == 2))
-            return launch_prefill_duo<DP>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+        if (nw == 8 && prefill_persist() && !prefill_pack(Hq, Hkv, Sq) && Sk > KT &&
+            ((Sk + KT - 1) / KT) % 2 == 0 &&
+            (long)Hq * ((Sq + 255) / 256) >= 2L * device_cus() && (long)Sq * D * 4 < 0x7fffffffL)
+            return launch_prefill_persist<DP>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,

@@ -7,6 +7,7 @@
 //   roofline_bench clock           MFMA-only rate and shader clock, constant vs random operands
 //   roofline_bench copy <MiB>      one float4 copy of <MiB> MiB (PMC calibration: known bytes)
 //   roofline_bench read <MiB>      streaming read of <MiB> MiB, ordinary and non-temporal loads
+//   roofline_bench mix             the headline prefill kernel's per-tile instruction mix, with parts removed
 //
 // Grid shapes are fixed at launch and every index is bounded by the buffer sizes below.
 #include <hip/hip_runtime.h>
@@ -282,6 +283,238 @@ __global__ __launch_bounds__(256) void lds_rate(unsigned *out, unsigned long lon
     const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     out[blockIdx.x * blockDim.x + threadIdx.x] = acc;
     if (threadIdx.x == 0) {
+        clk[2 * blockIdx.x] = t1 - t0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
+}
+
+// The per-tile instruction mix of the headline prefill kernel (attn_prefill_fast_kernel at
+// D = 128, 128-key tiles, 8 waves = two per SIMD, one workgroup per CU) without its data
+// dependencies on real inputs: per wave and tile, 32 MFMA of S^T = K.Q^T whose A operands are
+// 16-byte LDS reads of a K tile, the softmax VALU on those accumulators (p = 2^(s c - m c),
+// bf16 conversion, pairwise sums), 32 MFMA of O^T += V^T.P^T whose A operands are pairs of
+// transposed 8-byte LDS reads of a V tile, then (DMA) the next tile's 64 KB by LDS-DMA from an
+// L2-resident buffer and one barrier. LDS and register operands hold random bf16 (bounded
+// exponents), so the MFMA operand bits toggle as in the kernel. Switches take parts away:
+// REUSE = 2 reads each K and V fragment once for two MFMAs (half the LDS fragment bytes, as
+// with 64 rows per wave), VALU = false drops the softmax (P is then the S bits), DMA = false the
+// tile loads. The rate with everything on is the ceiling of this mix; each switch measures the
+// share of one resource. Every LDS address stays inside the two 64 KB tile buffers and every
+// DMA source offset inside src (64 KB per buffer, blocks of 1 KB per wave).
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_m;
+typedef __attribute__((ext_vector_type(4))) short s16x4_m;
+template <int REUSE, int VALU, bool DMA>
+__global__ __launch_bounds__(512, 1) void mix_tile(const unsigned short *src, float *out,
+                                                   unsigned long long *clk, int tiles) {
+    __shared__ __attribute__((aligned(1024))) unsigned short T[2][2][128 * 128]; // [buf][K,V]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
+    for (int i = tid; i < 2 * 2 * 128 * 128 / 8; i += 512)
+        reinterpret_cast<u32x4_m *>(&T[0][0][0])[i] =
+            reinterpret_cast<const u32x4_m *>(src)[i & (2 * 128 * 128 / 8 - 1)];
+    bf16x8 qb[8];
+    for (int k = 0; k < 8; ++k)
+        qb[k] = __builtin_bit_cast(bf16x8, reinterpret_cast<const u32x4_m *>(src)[lane * 8 + k]);
+    // fragment offsets as in the kernel's swizzled tiles (conflict-free)
+    const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int kfo = (kperm >> 3) * 8 * 128 + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
+    const int vfo = hi * 8 * 128 + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
+                    (i16 & 1) * 4;
+    const float c = 0.1275f;
+    float mrun = 4.0f, l = 0.f;
+    f32x16 o[4] = {}, negm;
+    for (int i = 0; i < 16; ++i)
+        negm[i] = -mrun * c;
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        if (DMA) {
+            // 64 KB per CU: each wave 4 K and 4 V blocks of 1 KB into the other buffer
+            const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<unsigned short *>(src), (short)0, 2 * 128 * 128 * 2, 0x00020000);
+            for (int k = 0; k < 4; ++k) {
+                const int blk = w * 4 + k; // 0..31
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r, (__attribute__((address_space(3))) void *)&T[buf ^ 1][0][blk * 512], 16,
+                    (unsigned)(blk * 1024 + lane * 16), 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r, (__attribute__((address_space(3))) void *)&T[buf ^ 1][1][blk * 512], 16,
+                    (unsigned)(32768 + blk * 1024 + lane * 16), 0, 0, 0);
+            }
+        }
+        const unsigned short *kb = &T[buf][0][kfo];
+        f32x16 s[4];
+        for (int st = 0; st < 4; ++st) {
+            for (int i = 0; i < 16; ++i)
+                s[st][i] = (VALU == 2) ? negm[i] : 0.f;
+            for (int kk = 0; kk < 8; kk += REUSE) {
+                const bf16x8 a = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4_m *>(kb + st * 32 * 128 + kk * 128));
+                for (int j = 0; j < REUSE; ++j)
+                    s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[(kk + j + st) & 7], s[st],
+                                                                    0, 0, 0);
+            }
+        }
+        bf16x8 pk[8];
+        if (VALU) {
+            const float mc = mrun * c;
+            float ps = 0.f;
+            for (int st = 0; st < 4; ++st)
+                for (int hh = 0; hh < 2; ++hh) {
+                    float p[8];
+                    for (int j = 0; j < 8; ++j) {
+                        p[j] = __builtin_amdgcn_exp2f(VALU == 2 ? s[st][8 * hh + j]
+                                                                : fmaf(s[st][8 * hh + j], c, -mc));
+                        pk[2 * st + hh][j] = (__bf16)p[j];
+                    }
+                    ps += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                }
+            l += ps;
+        } else {
+            for (int st = 0; st < 4; ++st)
+                for (int hh = 0; hh < 2; ++hh) {
+                    u32x4_m v;
+                    for (int j = 0; j < 4; ++j)
+                        v[j] = (__builtin_bit_cast(unsigned, s[st][8 * hh + 2 * j]) & 0x807F807Fu) |
+                               0x3C003C00u;
+                    pk[2 * st + hh] = __builtin_bit_cast(bf16x8, v);
+                }
+        }
+        const unsigned short *vb = &T[buf][1][vfo];
+        for (int cc = 0; cc < 8; ++cc)
+            for (int db = 0; db < 4; db += REUSE) {
+                const unsigned short *p = vb + cc * 16 * 128 + db * 128;
+                const s16x4_m lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_m *)p);
+                const s16x4_m hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_m *)(p + 4 * 128));
+                typedef __attribute__((ext_vector_type(8))) short s16x8;
+                const s16x8 a8 = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+                for (int j = 0; j < REUSE; ++j)
+                    o[db + j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[cc], o[db + j], 0, 0, 0);
+            }
+        if (DMA)
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float acc = l;
+    for (int d = 0; d < 4; ++d)
+        for (int i = 0; i < 16; ++i)
+            acc += o[d][i];
+    out[blockIdx.x * 512 + tid] = acc;
+    if (tid == 0) {
+        clk[2 * blockIdx.x] = t1 - t0;
+        clk[2 * blockIdx.x + 1] = r1 - r0;
+    }
+}
+
+// The same per-tile mix for one wave per SIMD with 64 query rows (4 waves per CU, 512
+// registers each): every K and V fragment read from LDS feeds two MFMAs (the two 32-row
+// blocks), the softmax covers 128 scores per lane. Per CU and tile the MFMA work equals
+// mix_tile's; the LDS fragment bytes are half.
+template <bool VALU>
+__global__ __launch_bounds__(256, 1) void mix_tile_w64(const unsigned short *src, float *out,
+                                                       unsigned long long *clk, int tiles) {
+    __shared__ __attribute__((aligned(1024))) unsigned short T[2][2][128 * 128]; // [buf][K,V]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
+    for (int i = tid; i < 2 * 2 * 128 * 128 / 8; i += 256)
+        reinterpret_cast<u32x4_m *>(&T[0][0][0])[i] =
+            reinterpret_cast<const u32x4_m *>(src)[i & (2 * 128 * 128 / 8 - 1)];
+    bf16x8 qb[2][8];
+    for (int rb = 0; rb < 2; ++rb)
+        for (int k = 0; k < 8; ++k)
+            qb[rb][k] = __builtin_bit_cast(
+                bf16x8, reinterpret_cast<const u32x4_m *>(src)[(lane * 8 + k + rb * 1024) & 4095]);
+    const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int kfo = (kperm >> 3) * 8 * 128 + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
+    const int vfo = hi * 8 * 128 + (i16 >> 2) * 32 + (2 * (g16 & 1) + ((i16 & 3) >> 1)) * 8 +
+                    (i16 & 1) * 4;
+    const float c = 0.1275f;
+    float mrun = 4.0f, l = 0.f;
+    f32x16 o[2][4] = {};
+    __syncthreads();
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned short *>(src), (short)0, 2 * 128 * 128 * 2, 0x00020000);
+        for (int k = 0; k < 8; ++k) { // 64 KB per CU: each of 4 waves 8 K and 8 V blocks
+            const int blk = w * 8 + k;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                r, (__attribute__((address_space(3))) void *)&T[buf ^ 1][0][blk * 512], 16,
+                (unsigned)(blk * 1024 + lane * 16), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                r, (__attribute__((address_space(3))) void *)&T[buf ^ 1][1][blk * 512], 16,
+                (unsigned)(32768 + blk * 1024 + lane * 16), 0, 0, 0);
+        }
+        const unsigned short *kb = &T[buf][0][kfo];
+        const unsigned short *vb = &T[buf][1][vfo];
+        // per 32-key sub-tile: S for both row blocks, softmax, P.V
+        for (int st = 0; st < 4; ++st) {
+            f32x16 s[2];
+            for (int rb = 0; rb < 2; ++rb)
+                for (int i = 0; i < 16; ++i)
+                    s[rb][i] = 0.f;
+            for (int kk = 0; kk < 8; ++kk) {
+                const bf16x8 a = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4_m *>(kb + st * 32 * 128 + kk * 128));
+                for (int rb = 0; rb < 2; ++rb)
+                    s[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[rb][kk], s[rb], 0, 0, 0);
+            }
+            bf16x8 pk[2][2];
+            if (VALU) {
+                const float mc = mrun * c;
+                float ps = 0.f;
+                for (int rb = 0; rb < 2; ++rb)
+                    for (int hh = 0; hh < 2; ++hh) {
+                        float p[8];
+                        for (int j = 0; j < 8; ++j) {
+                            p[j] = __builtin_amdgcn_exp2f(fmaf(s[rb][8 * hh + j], c, -mc));
+                            pk[rb][hh][j] = (__bf16)p[j];
+                        }
+                        ps += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                    }
+                l += ps;
+            } else {
+                for (int rb = 0; rb < 2; ++rb)
+                    for (int hh = 0; hh < 2; ++hh) {
+                        u32x4_m v;
+                        for (int j = 0; j < 4; ++j)
+                            v[j] = (__builtin_bit_cast(unsigned, s[rb][8 * hh + 2 * j]) & 0x807F807Fu) |
+                                   0x3C003C00u;
+                        pk[rb][hh] = __builtin_bit_cast(bf16x8, v);
+                    }
+            }
+            for (int hh = 0; hh < 2; ++hh)
+                for (int db = 0; db < 4; ++db) {
+                    const unsigned short *p = vb + (st * 2 + hh) * 16 * 128 + db * 128;
+                    const s16x4_m lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4_m *)p);
+                    const s16x4_m hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4_m *)(p + 4 * 128));
+                    typedef __attribute__((ext_vector_type(8))) short s16x8;
+                    const s16x8 a8 = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                    const bf16x8 a = __builtin_bit_cast(bf16x8, a8);
+                    for (int rb = 0; rb < 2; ++rb)
+                        o[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pk[rb][hh], o[rb][db],
+                                                                            0, 0, 0);
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float acc = l;
+    for (int rb = 0; rb < 2; ++rb)
+        for (int d = 0; d < 4; ++d)
+            for (int i = 0; i < 16; ++i)
+                acc += o[rb][d][i];
+    out[blockIdx.x * 512 + tid] = acc;
+    if (tid == 0) {
         clk[2 * blockIdx.x] = t1 - t0;
         clk[2 * blockIdx.x + 1] = r1 - r0;
     }
@@ -599,6 +832,61 @@ static double run_lds(bool tr, int wpc) {
     return best;
 }
 
+// mix_tile over one workgroup per CU: TFLOP/s of its MFMA work, the shader clock (s_memtime
+// over the 100 MHz s_memrealtime) and shader clocks per tile, best of three runs.
+template <int REUSE, int VALU, bool DMA, bool W64 = false>
+static void run_mix(double *tflops, double *ghz, double *clk_per_tile) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus, tiles = 2000;
+    std::vector<unsigned short> h(2 * 128 * 128);
+    unsigned x = 0x2468ace1u;
+    for (auto &e : h) {
+        x ^= x << 13; x ^= x >> 17; x ^= x << 5;
+        e = (unsigned short)((x & 0x807Fu) | 0x3F00u); // random sign and mantissa, |v| in [0.5, 1)
+    }
+    unsigned short *src;
+    float *out;
+    unsigned long long *clk;
+    CHECK(hipMalloc(&src, h.size() * 2));
+    CHECK(hipMalloc(&out, (size_t)blocks * 512 * sizeof(float)));
+    CHECK(hipMalloc(&clk, (size_t)blocks * 2 * sizeof(unsigned long long)));
+    CHECK(hipMemcpy(src, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+    std::vector<unsigned long long> hc((size_t)blocks * 2);
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    *tflops = 0;
+    for (int rep = 0; rep < 3; ++rep) {
+        CHECK(hipEventRecord(a, 0));
+        if (W64)
+            hipLaunchKernelGGL((mix_tile_w64<VALU != 0>), dim3(blocks), dim3(256), 0, 0, src, out, clk,
+                               tiles);
+        else
+            hipLaunchKernelGGL((mix_tile<REUSE, VALU, DMA>), dim3(blocks), dim3(512), 0, 0, src,
+                               out, clk, tiles);
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        const double ms = time_ms(a, b);
+        const double tf = (double)blocks * 8 * 64 * tiles * 32768.0 / (ms * 1e-3) / 1e12;
+        if (tf > *tflops) {
+            *tflops = tf;
+            CHECK(hipMemcpy(hc.data(), clk, hc.size() * sizeof(unsigned long long),
+                            hipMemcpyDeviceToHost));
+            double g = 0, cpt = 0;
+            for (int i = 0; i < blocks; ++i) {
+                g += (double)hc[2 * i] / (double)hc[2 * i + 1] * 0.1 / blocks;
+                cpt += (double)hc[2 * i] / tiles / blocks;
+            }
+            *ghz = g;
+            *clk_per_tile = cpt;
+        }
+    }
+    CHECK(hipFree(src));
+    CHECK(hipFree(out));
+    CHECK(hipFree(clk));
+}
+
 static double run_stream(int copy, size_t mib, int reps, bool nt = false) {
     size_t bytes = mib << 20, n4 = bytes / 16;
     f32x4 *src, *dst;
@@ -679,6 +967,26 @@ int main(int argc, char **argv) {
             printf("{\"waves_per_cu\": %d, \"lds_read_b128_bytes_per_clk_cu\": %.1f, "
                    "\"lds_read_tr_b64_bytes_per_clk_cu\": %.1f}\n",
                    wpc, run_lds(false, wpc), run_lds(true, wpc));
+    } else if (!strcmp(mode, "mix")) {
+        struct {
+            const char *name;
+            void (*fn)(double *, double *, double *);
+        } v[] = {{"kernel mix (1 KB LDS per MFMA, softmax VALU, DMA)", run_mix<1, true, true>},
+                 {"softmax without the fma (scale in Q, max in the accumulators)", run_mix<1, 2, true>},
+                 {"half the LDS fragment reads", run_mix<2, true, true>},
+                 {"no softmax VALU", run_mix<1, false, true>},
+                 {"no DMA", run_mix<1, true, false>},
+                 {"half LDS reads, no softmax VALU", run_mix<2, false, true>},
+                 {"MFMA and LDS reads only", run_mix<1, false, false>},
+                 {"one wave per SIMD, 64 rows (half the LDS fragment reads)", run_mix<2, true, true, true>},
+                 {"one wave per SIMD, 64 rows, no softmax VALU", run_mix<2, false, true, true>}};
+        for (auto &e : v) {
+            double tf, g, cpt;
+            e.fn(&tf, &g, &cpt);
+            printf("{\"mix\": \"%s\", \"tflops\": %.1f, \"ghz\": %.3f, "
+                   "\"shader_clocks_per_tile\": %.0f, \"mfma_clocks_per_tile\": 4096}\n",
+                   e.name, tf, g, cpt);
+        }
     } else if (!strcmp(mode, "valu")) {
         printf("{\"exp_chain_steps_per_simd_clk\": %.4f, \"fma_per_simd_clk\": %.4f}\n",
                run_valu(true), run_valu(false));
@@ -695,7 +1003,7 @@ int main(int argc, char **argv) {
                "\"copy_gbps\": %.1f, \"read_gbps\": %.1f, \"stream_mib\": %zu}\n",
                m32, m16, mr, cp, rd, mib);
     } else {
-        fprintf(stderr, "usage: %s [all|mfma|clock|split|coissue|chain|lds|valu|copy MiB|read MiB]\n", argv[0]);
+        fprintf(stderr, "usage: %s [all|mfma|clock|split|coissue|chain|lds|mix|valu|copy MiB|read MiB]\n", argv[0]);
         return 2;
     }
     return 0;
