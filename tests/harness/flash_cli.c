@@ -664,10 +664,11 @@ int main(int argc, char **argv) {
     struct shape custom;
     if (cfg.shape_text && !parse_shape(cfg.shape_text, &custom))
         return EXIT_BAD_USAGE;
-    if (cfg.warmup < 0)
-        cfg.warmup = 0;
-    if (cfg.iters < 0)
-        cfg.iters = 0;
+    if (cfg.iters < 0 || cfg.warmup < 0 || cfg.llc_mib < 0) {
+        printf("flash_cli: --iters, --warmup and --llc-mb must be >= 0 (got %d, %d, %d)\n",
+               cfg.iters, cfg.warmup, cfg.llc_mib);
+        return EXIT_BAD_USAGE;
+    }
     if (!(cfg.min_secs > 0.0))
         cfg.min_secs = 0.5;
     if (cfg.pick_selftest)

@@ -49,6 +49,9 @@ def run(cli, *args, timeout=300):
     (["--shape", "4,4,8,8,257"], "above ATTN_D_MAX=256"),
     (["--shape", "4,4,8,8,64,1,-1"], "ref_cap must be >= 0"),
     (["--iters", "3.5"], "wants an integer"),
+    (["--iters", "-5"], "must be >= 0"),
+    (["--warmup", "-1"], "must be >= 0"),
+    (["--llc-mb", "-16"], "must be >= 0"),
     (["--bench-secs", "fast"], "wants a number"),
     (["--frobnicate"], "unrecognised option '--frobnicate'"),
     (["--no-softmax"], "--no-softmax is rejected"),

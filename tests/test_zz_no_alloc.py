@@ -2,7 +2,8 @@
 library's static device array instead of a caller's scratch. Each case runs two calls in a row
 through the C ABI, the second with a smaller input (so stale partials of the first call would
 show), and each output must equal attn_flash's with a caller-owned scratch bit for bit (same
-kernels, same splits, same slot layout), and pass the oracle on spread rows."""
+kernels, same splits, same slot layout), and pass the oracle on spread rows. Every case takes a
+path that writes partials: attn_flash's scratch, poisoned before its call, must have changed."""
 import sys
 
 import numpy as np
@@ -26,7 +27,8 @@ def _gpu_present():
 
 
 def run_both(Hq, Hkv, Sq, Sk, D, causal, seed, v_prepacked=0):
-    """(O from attn_flash with its own scratch, O from attn_flash_noalloc, host inputs)."""
+    """(O from attn_flash with its own scratch, O from attn_flash_noalloc, host inputs, bytes of
+    attn_flash's scratch that its call changed)."""
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, seed)
     Vin = V.reshape(Hkv, Sk, D).transpose(0, 2, 1).copy().ravel() if v_prepacked else V
     outs = []
@@ -34,24 +36,31 @@ def run_both(Hq, Hkv, Sq, Sk, D, causal, seed, v_prepacked=0):
             ts.DeviceBuffer.from_array(Vin) as dv, ts.DeviceBuffer(Hq * Sq * D * 4) as do, \
             ts.DeviceBuffer(ts.attn_flash_scratch_bytes(D, 128)) as ds:
         do.fill_bytes(0xFF)
+        ds.fill_bytes(0xFF)
         ts.attn_flash(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, causal, 128, ds, v_prepacked)
         ts.synchronize()
         outs.append(do.download(np.float32))
+        changed = int(np.count_nonzero(ds.download(np.uint8) != 0xFF))
         do.fill_bytes(0xFF)
         ts.attn_flash_noalloc(dq, dk, dv, do, Hq, Hkv, Sq, Sk, D, causal, 128, v_prepacked)
         ts.synchronize()
         outs.append(do.download(np.float32))
-    return outs[0], outs[1], (Q, K, V)
+    return outs[0], outs[1], (Q, K, V), changed
 
 
-# (label, Hq, Hkv, Sq, Sk, D, causal, v_prepacked): pairs of a larger then a smaller call on
-# paths that use the partial slots (split-K decode + merge; causal prefill with split key
-# ranges + merge), then a prefill that uses none.
+# (label, Hq, Hkv, Sq, Sk, D, causal, v_prepacked): pairs of a larger then a smaller call, each
+# on a path that writes partial slots and merges them: split-K decode (row-major V and V^T),
+# the causal prefill's split of its upper query tiles, the prefill key split of small grids, and
+# the slot-balanced head split (D <= 64).
 PAIRS = [
     (("decode split 32k", 32, 8, 1, 32768, 128, 0, 0),
      ("decode split 4k", 32, 8, 1, 4096, 128, 0, 0)),
-    (("qwen3 causal split 2k", 16, 8, 2048, 2048, 128, 1, 0),
-     ("qwen3 causal split 1k", 16, 8, 1024, 1024, 128, 1, 0)),
+    (("prefill causal split 2k", 8, 2, 2048, 2048, 128, 1, 0),
+     ("prefill causal split 2k MQA", 4, 1, 2048, 2048, 128, 1, 0)),
+    (("prefill key split 8k causal", 32, 8, 512, 8192, 128, 1, 0),
+     ("prefill key split 4k", 16, 4, 512, 4096, 128, 0, 0)),
+    (("prefill head split D64", 48, 12, 1000, 4000, 64, 0, 0),
+     ("prefill head split D40", 20, 5, 1800, 2056, 40, 0, 0)),
     (("decode split 8k D64 V^T", 16, 4, 4, 8192, 64, 1, 1),
      ("decode split 1k D40", 8, 2, 2, 1000, 40, 0, 0)),
 ]
@@ -62,7 +71,9 @@ def test_noalloc_matches_attn_flash_twice(oracle, pair):
     for i, (label, Hq, Hkv, Sq, Sk, D, causal, vt) in enumerate(pair):
         say("noalloc case %s (call %d): Hq=%d Hkv=%d Sq=%d Sk=%d D=%d causal=%d vt=%d" %
             (label, i + 1, Hq, Hkv, Sq, Sk, D, causal, vt))
-        ref, got, (Q, K, V) = run_both(Hq, Hkv, Sq, Sk, D, causal, SEED0 + 17 * i, vt)
+        ref, got, (Q, K, V), changed = run_both(Hq, Hkv, Sq, Sk, D, causal, SEED0 + 17 * i, vt)
+        say("   %d scratch bytes written by attn_flash" % changed)
+        assert changed > 0, label  # the case must exercise the partial slots
         assert np.all(np.isfinite(got)), label
         assert np.array_equal(ref, got), label
         rows = oracle.ref_rowset(Sq, 8)

@@ -2606,7 +2606,7 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
                : 8;
 }
 
-// Key halves (attn_prefill_fast_kernel's KH): where 4-wave workgroups would run at D > 64, an
+// Key halves (attn_prefill_fast_kernel's KH): where 4-wave workgroups would run at D >= 64, an
 // 8-wave workgroup serves the same 128 rows with 128-key tiles, each SIMD's two waves taking
 // the two halves of every tile. Taken where it measured faster (same box, two runs each):
 // non-causal grids of at most one 128-row tile per CU (16 heads at 2k 54.3 -> 39.8 us; there
@@ -2625,20 +2625,20 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
 // c4 0.284 -> 0.319 ms): twice the workgroups, each with its fixed cost and a merge.
 // At D = 64 (4-wave workgroups there keep 128-key tiles, two per CU) it measured: 32 heads at
 // 1k 27.7 -> 15.7 us, 16 heads at 2k 37.4 -> 25.5 us, 24 heads of 512 rows over 4000 keys
-// +18%, 16 heads at 2k / 4k causal +14% / +7%; config 1 (two key tiles) 6.5 -> 7.0 us, so key
-// halves need at least four key tiles. Slot-balanced head-split grids keep 4 waves.
-// ATTN_PREFILL_KH=0 (read once) keeps the 4-wave,
-// 64-key-tile workgroups and =2 takes key halves wherever 4 waves run at D > 64 (with
-// ATTN_PREFILL_WAVES=4: everywhere), for tuning sweeps.
-static bool prefill_kh(int Hq, int Sq, int Sk, bool causal) {
+// +18%, 16 heads at 2k / 4k causal +14% / +7%; config 1 (two key tiles) 6.5 -> 7.0 us, so at
+// D = 64 key halves need at least four key tiles (no such limit was measured at D > 64, where
+// the 4-wave alternative takes 64-key tiles). Slot-balanced head-split grids keep 4 waves.
+// ATTN_PREFILL_KH=0 (read once) keeps the 4-wave workgroups and =2 takes key halves wherever
+// 4 waves run at D >= 64 (with ATTN_PREFILL_WAVES=4: everywhere), for tuning sweeps.
+static bool prefill_kh(int DP, int Hq, int Sq, int Sk, bool causal) {
     static int env = -1;
     if (env < 0) {
         const char *e = getenv("ATTN_PREFILL_KH");
         env = (e && (atoi(e) == 0 || atoi(e) == 2)) ? atoi(e) : 1;
     }
     const long n = (long)Hq * ((Sq + 127) / 128), cus = device_cus();
-    return env == 2 ||
-           (env == 1 && Sk > 3 * 128 && (n <= cus || (causal && n == 2 * cus)));
+    return env == 2 || (env == 1 && (DP > 64 || Sk > 3 * 128) &&
+                        (n <= cus || (causal && n == 2 * cus)));
 }
 
 // ATTN_PREFILL_KT=64 or =128 (read once) forces the prefill key tile for tuning sweeps: 64 keys
@@ -2699,7 +2699,7 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                                                   c, pm, pl, pacc, slots, st);
     }
     if constexpr (DP >= 64 && DP <= 128 && KT == 128)
-        if (nw == 4 && !hs && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(Hq, Sq, Sk, CAUSAL))
+        if (nw == 4 && !hs && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(DP, Hq, Sq, Sk, CAUSAL))
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
