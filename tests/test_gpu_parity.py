@@ -400,6 +400,7 @@ def test_prefill_head_split(oracle, Hq, Hkv, Sq, Sk, D, sigma_q, ref_cap):
     (8, 2, 600, 2104, 64, 0),
     (4, 1, 1024, 1024, 128, 1),   # causal small grid: upper query tiles split over two items
     (128, 32, 1024, 1504, 128, 0),  # the persistent prefill (12 key tiles per item)
+    (128, 32, 1024, 1024, 128, 1),  # the causal persistent prefill (pairs of 2 + 8, 4 + 6 tiles)
 ])
 def test_score_jumps_between_key_tiles(oracle, Hq, Hkv, Sq, Sk, D, causal):
     """Each query row gets a first coordinate of +4 or -4 and each key a first coordinate that
@@ -626,24 +627,27 @@ sys.path.insert(0, %r)
 import transfer_station_amd as ts
 from oracle import oracle as o
 out = []
-for i, (Hq, Hkv, Sq, Sk, D, sigma, vt) in enumerate(%r):
+for i, (Hq, Hkv, Sq, Sk, D, sigma, causal) in enumerate(%r):
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 313 + i, sigma_q=sigma)
-    O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128, prepack_v=bool(vt))
+    O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, 128)
     rows = o.ref_rowset(Sq, 8)
-    R = o.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, rows, nthreads=8)
+    R = o.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, rows, nthreads=8)
     ok, mad, maxref, nbad = o.cmp_rows(R, O, Hq, Sq, D, rows)
-    print("persist case", Hq, Hkv, Sq, Sk, D, sigma, vt, mad / maxref, nbad, flush=True)
+    print("persist case", Hq, Hkv, Sq, Sk, D, sigma, causal, mad / maxref, nbad, flush=True)
     assert ok
     out.append(O)
 np.savez(%r, *out)
 print("OK")
 """
 
-# Shapes that take the persistent prefill on a 256-CU part (non-causal, 97 <= D <= 128, an even
-# number of 128-key tiles, at least two 256-row items per CU): uneven items per workgroup, a
-# ragged last query tile, two key tiles (the first tile followed by the last), D = 104, peaked
-# scores (sigma_q = 4: the lazy-sum recompute), MHA with an item count that no XCD divides, and
-# MQA-like sharing (one kv head for 64 query heads). V^T (prepacked) keeps the per-tile kernel.
+# Shapes that take the persistent prefill on a 256-CU part (97 <= D <= 128, at least two 256-row
+# items per CU, an even number of 128-key tiles per item; causal: Sk >= Sq and an even number of
+# query tiles), as (Hq, Hkv, Sq, Sk, D, sigma_q, causal). Non-causal: uneven items per
+# workgroup, a ragged last query tile, two key tiles (the first tile followed by the last),
+# D = 104, peaked scores (sigma_q = 4: the lazy-sum recompute), MHA with an item count that no
+# XCD divides, MQA-like sharing (one kv head for 64 query heads). Causal (pairs of query tiles):
+# a ragged last query tile and key tail, keys before the query block with peaked scores,
+# D = 104, and GQA 4 at 2k. V^T (prepacked) keeps the per-tile kernel.
 PERSIST_CASES = [
     (128, 32, 1000, 1000, 128, 1.0, 0),
     (256, 16, 512, 256, 128, 1.0, 0),
@@ -651,6 +655,10 @@ PERSIST_CASES = [
     (192, 48, 700, 900, 128, 4.0, 0),
     (131, 131, 1024, 512, 128, 1.0, 0),
     (128, 2, 1024, 1024, 128, 1.0, 0),
+    (128, 32, 1000, 1000, 128, 1.0, 1),
+    (128, 32, 1024, 2048, 128, 4.0, 1),
+    (128, 32, 1024, 1024, 104, 1.0, 1),
+    (64, 16, 2048, 2048, 128, 1.0, 1),
 ]
 
 

@@ -1278,7 +1278,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // the wave are in flight, with no wait on expcnt or lgkmcnt.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-template <int DP>
+template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
@@ -1297,27 +1297,48 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
 
     const int g = Hq / Hkv;
     const int b = wg_id_x(), x = b & 7, xi = b >> 3, R = nwg >> 3; // nwg % 8 == 0
+    // nitems units (items, or causal pairs of items) dealt to the XCDs in contiguous runs.
     const int per = nitems >> 3, rem = nitems & 7;
     const int xb = (x < rem) ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
     const int nx = per + (x < rem ? 1 : 0);
-    const int nmine = (xi < nx) ? (nx - xi + R - 1) / R : 0;
+    const int nunits = (xi < nx) ? (nx - xi + R - 1) / R : 0;
+    const int nmine = CAUSAL ? 2 * nunits : nunits; // items of this workgroup
     if (nmine == 0)
         return;
-    // Item k of this workgroup: query head h and 256-row tile qt (the fast kernel's non-causal
-    // order: kv head, then tile, then the g heads of the group).
+    // Item k of this workgroup: query head h and 256-row tile qt. Non-causal: the fast kernel's
+    // order (kv head, then tile, then the g heads of the group). Causal (nqt even): unit P is
+    // the pair of tiles nqt-1-p and p of one head (kv head, then p, then the head), whose key
+    // tiles add up to the same count for every p, run heavy first: each workgroup gets the
+    // same number of pairs and so the same work.
     auto item = [&](int k, int &h, int &qt) {
-        const int L = xb + xi + k * R;
-        const int uu = L / (g * nqt);
-        const int rr = L - uu * (g * nqt);
-        qt = __builtin_amdgcn_readfirstlane(rr / g);
-        h = __builtin_amdgcn_readfirstlane(uu * g + (rr - (rr / g) * g));
+        if constexpr (CAUSAL) {
+            const int np = nqt >> 1;
+            const int P = xb + xi + (k >> 1) * R;
+            const int uu = P / (g * np);
+            const int rr = P - uu * (g * np);
+            const int pp = rr / g;
+            qt = __builtin_amdgcn_readfirstlane((k & 1) ? pp : nqt - 1 - pp);
+            h = __builtin_amdgcn_readfirstlane(uu * g + (rr - pp * g));
+        } else {
+            const int L = xb + xi + k * R;
+            const int uu = L / (g * nqt);
+            const int rr = L - uu * (g * nqt);
+            qt = __builtin_amdgcn_readfirstlane(rr / g);
+            h = __builtin_amdgcn_readfirstlane(uu * g + (rr - (rr / g) * g));
+        }
     };
 
     const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     // & 7: the compiler then knows each wave's DMA blocks stay inside one tile buffer
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & 7;
     const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
-    const int nkt = (Sk + KT - 1) / KT; // even (host)
+    // Key tiles of an item: all of them, or (causal) those up to its last row's limit,
+    // Sk - Sq + its last row (Sk >= Sq). Even for every item (host).
+    auto nkt_of = [&](int qt) {
+        if constexpr (CAUSAL)
+            return (Sk - Sq + min(Sq - 1, qt * BQ + BQ - 1)) / KT + 1;
+        return (Sk + KT - 1) / KT;
+    };
 
     const uint32_t qbytes = (uint32_t)Sq * (uint32_t)D * 2u; // one head of Q (O: twice; < 2^31)
     // Q rows of item (h, qt) for this lane's operand layout: 16-byte buffer loads, rows past Sq
@@ -1424,26 +1445,57 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
         }
     };
-    // Keys at or past Sk (an item's last tile only) take -inf: sub-tiles wholly before Sk are
-    // skipped and sub-tiles wholly past it set at once (wave-uniform tests), so only the
-    // sub-tile that Sk crosses is compared key by key.
-    auto mask = [&](int kbase) __attribute__((always_inline)) {
-        if (kbase + KT > Sk) {
+    // Keys past a row's limit take -inf: Sk - 1, or (causal) min(Sk - 1, Sk - Sq + row). The
+    // wave's rows qmin .. qmin + 31 of item tile qt have limits from lo (its first row's) to
+    // wmax (its last valid row's; -1 when it has none); sub-tiles wholly at or below lo are
+    // skipped and sub-tiles wholly past wmax set at once (wave-uniform tests), so only a
+    // sub-tile between the two is compared key by key.
+    auto lims = [&](int qt, int &lo, int &wmax) {
+        if constexpr (CAUSAL) {
+            const int qmin = qt * BQ + w * 32;
+            lo = __builtin_amdgcn_readfirstlane(min(Sk - 1, Sk - Sq + qmin));
+            wmax = __builtin_amdgcn_readfirstlane(
+                qmin < Sq ? min(Sk - 1, Sk - Sq + min(Sq - 1, qmin + 31)) : -1);
+        } else {
+            lo = Sk - 1;
+            wmax = Sk - 1;
+        }
+    };
+    auto mask = [&](int kbase, int qt) __attribute__((always_inline)) {
+        int lo, wmax;
+        lims(qt, lo, wmax);
+        if (kbase + KT - 1 > lo) {
+            int lim = Sk - 1;
+            if constexpr (CAUSAL) {
+                int r = w * 32 + l32;
+                asm volatile("" : "+v"(r));
+                lim = min(Sk - 1, Sk - Sq + qt * BQ + r);
+            }
 #pragma unroll
             for (int t = 0; t < KT / 32; ++t) {
                 const int k0t = kbase + t * 32;
-                if (k0t + 32 <= Sk)
+                if (k0t + 31 <= lo)
                     continue;
-                if (k0t >= Sk) {
+                if (k0t > wmax) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
                         s[t][i] = kNegInf;
                     continue;
                 }
+                if constexpr (CAUSAL) {
+                    // key = k0t + 8 hi + 16 (i >> 3) + (i & 7) > lim, against one register and
+                    // immediates (with the keys in registers the causal variant spills)
+                    const int rel = lim - k0t - 8 * hi;
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (k0t + 16 * (i >> 3) + 8 * hi + (i & 7) >= Sk)
-                        s[t][i] = kNegInf;
+                    for (int i = 0; i < 16; ++i)
+                        if (16 * (i >> 3) + (i & 7) > rel)
+                            s[t][i] = kNegInf;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (k0t + 16 * (i >> 3) + 8 * hi + (i & 7) > lim)
+                            s[t][i] = kNegInf;
+                }
             }
         }
     };
@@ -1549,14 +1601,16 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     }
     __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): Q and tile 0 of the first item
     __syncthreads();
-    // One key tile of item k (kv head u): FIRST (kt = 0: the previous item's O leaves, then the
-    // row max), LAST (kt = nkt - 1: the next item's tile 0 DMA and Q loads, the Sk mask, the row
-    // max) or neither (the sum test, a rare recompute). Item coordinates are recomputed from
-    // the item index where needed rather than carried in registers.
-    // nkt is even (host), so tile kt of every item uses LDS buffer kt & 1: each step's buffers
+    // One key tile kt of item k (kv head u, query tile qt): FIRST (kt = 0: the previous item's
+    // O leaves, then the row max), LAST (kt = nkt - 1: the next item's tile 0 DMA and Q loads,
+    // the mask, the row max) or neither (the sum test, a rare recompute). Item coordinates are
+    // recomputed from the item index where needed rather than carried in registers.
+    // Every item's nkt is even (host), so tile kt uses LDS buffer kt & 1: each step's buffers
     // are constants, which lets the compiler tell this tile's LDS reads from the next tile's DMA
     // (with a run-time buffer index it waits for that DMA before the first read).
-    auto step = [&](int u, int kt, int k, auto kbuf, auto kfirst, auto klast)
+    // Causal: FIRST and middle tiles are masked too where they reach past the wave's first
+    // row's limit.
+    auto step = [&](int u, int qt, int kt, int k, auto kbuf, auto kfirst, auto klast)
         __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(kfirst)::value, LAST = decltype(klast)::value;
         constexpr int buf = decltype(kbuf)::value;
@@ -1584,6 +1638,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
                 for (int i = 0; i < 16; ++i)
                     o[db][i] = 0.f;
         }
+        int kbase = kt * KT;
+        if constexpr (LAST || CAUSAL)
+            asm volatile("" : "+s"(kbase));
+        int lo, wmax;
+        lims(qt, lo, wmax);
+        // Causal: a wave whose rows see no key of the last tile (the first half of the waves
+        // when the query tile's limits are 128-key aligned) skips its softmax and P.V there
+        // but still computes S^T: skipping that too made the compiler spill about 100
+        // registers.
         qk(buf);
         pv_first(buf);
         // The fast kernel's phase order: S^T, then the softmax, then P.V (letting the compiler
@@ -1596,24 +1659,28 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             load_q(hn, qtn);
         }
         if (FIRST || LAST) {
-            if (LAST) {
-                int kbase = kt * KT;
-                asm volatile("" : "+s"(kbase));
-                mask(kbase);
+            if (!(CAUSAL && LAST) || kbase <= wmax) {
+                if (LAST || CAUSAL)
+                    mask(kbase, qt);
+                row_max();
+                l_run += exps();
             }
-            row_max();
-            l_run += exps();
         } else {
+            if constexpr (CAUSAL)
+                mask(kbase, qt);
             float psum = exps();
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(psum <= kSumCap)) != 0, 0)) {
                 qk(buf);
                 pv_first(buf);
+                if constexpr (CAUSAL)
+                    mask(kbase, qt);
                 row_max();
                 psum = exps();
             }
             l_run += psum;
         }
-        pv(buf);
+        if (!(CAUSAL && LAST) || kbase <= wmax)
+            pv(buf);
         if (!LAST || more) {
             // Wait for the next tile's DMA only: the O stores of tile 0 (NOST) are younger and
             // stay in flight. The last tile waits for everything (the next item's Q loads, issued
@@ -1631,14 +1698,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         int h, qt;
         item(k, h, qt);
         const int u = __builtin_amdgcn_readfirstlane(h / g);
+        const int nkt = __builtin_amdgcn_readfirstlane(nkt_of(qt));
         using B0 = std::integral_constant<int, 0>;
         using B1 = std::integral_constant<int, 1>;
-        step(u, 0, k, B0{}, std::true_type{}, std::false_type{});
+        step(u, qt, 0, k, B0{}, std::true_type{}, std::false_type{});
         for (int kt = 1; kt + 1 < nkt; kt += 2) {
-            step(u, kt, k, B1{}, std::false_type{}, std::false_type{});
-            step(u, kt + 1, k, B0{}, std::false_type{}, std::false_type{});
+            step(u, qt, kt, k, B1{}, std::false_type{}, std::false_type{});
+            step(u, qt, kt + 1, k, B0{}, std::false_type{}, std::false_type{});
         }
-        step(u, nkt - 1, k, B1{}, std::false_type{}, std::true_type{});
+        step(u, qt, nkt - 1, k, B1{}, std::false_type{}, std::true_type{});
     }
     {
         int hl, qtl;
@@ -2663,19 +2731,38 @@ static int prefill_persist() {
     return env;
 }
 
+// Whether a grid suits the persistent prefill: at least two items (256-row query tiles) per
+// CU; every item's key-tile count even and at least two (the kernel's compile-time buffer
+// order); causal: Sk >= Sq (every row sees key 0) and an even tile count (the pairs).
+static bool prefill_persist_fits(int Hq, int Sq, int Sk, int D, bool causal) {
+    const int nqt = (Sq + 255) / 256;
+    if ((long)Hq * nqt < 2L * device_cus() || (long)Sq * D * 4 >= 0x7fffffffL)
+        return false;
+    if (!causal)
+        return Sk > 128 && ((Sk + 127) / 128) % 2 == 0;
+    if (Sk < Sq || nqt % 2 != 0)
+        return false;
+    for (int qt = 0; qt < nqt; ++qt) {
+        const int nk = (Sk - Sq + std::min(Sq - 1, qt * 256 + 255)) / 128 + 1;
+        if (nk < 2 || nk % 2 != 0)
+            return false;
+    }
+    return true;
+}
+
 // One workgroup per CU (a multiple of 8: each XCD takes the same count), each running its
-// items of the 256-row tiling back to back.
-template <int DP>
+// items of the 256-row tiling back to back (causal: pairs of items).
+template <int DP, bool CAUSAL>
 hipError_t launch_prefill_persist(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
                                   hipStream_t st) {
     const int nqt = (Sq + 255) / 256;
-    const long nitems = (long)Hq * nqt;
+    const long nunits = (long)Hq * nqt / (CAUSAL ? 2 : 1);
     const int nwg = device_cus() / 8 * 8;
-    if (nitems <= 0 || nitems > 0x7fffffffL || nwg <= 0)
+    if (nunits <= 0 || nunits > 0x3fffffffL || nwg <= 0)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_persist_kernel<DP>), dim3((unsigned)nwg), dim3(512), 0, st,
-                       Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nitems, nwg);
+    hipLaunchKernelGGL((attn_prefill_persist_kernel<DP, CAUSAL>), dim3((unsigned)nwg), dim3(512),
+                       0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nunits, nwg);
     return hipGetLastError();
 }
 
@@ -2703,13 +2790,12 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
-    // Grids of at least two rounds of 8-wave workgroups with an even number (at least two) of
-    // key tiles per item and row-major V run persistent (attn_prefill_persist_kernel).
-    if constexpr (DP == 128 && KT == 128 && !CAUSAL && !VT)
-        if (nw == 8 && prefill_persist() && !prefill_pack(Hq, Hkv, Sq) && Sk > KT &&
-            ((Sk + KT - 1) / KT) % 2 == 0 &&
-            (long)Hq * ((Sq + 255) / 256) >= 2L * device_cus() && (long)Sq * D * 4 < 0x7fffffffL)
-            return launch_prefill_persist<DP>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+    // Grids of at least two rounds of 8-wave workgroups with row-major V whose items suit it
+    // run persistent (attn_prefill_persist_kernel).
+    if constexpr (DP == 128 && KT == 128 && !VT)
+        if (nw == 8 && prefill_persist() && !prefill_pack(Hq, Hkv, Sq) &&
+            prefill_persist_fits(Hq, Sq, Sk, D, CAUSAL))
+            return launch_prefill_persist<DP, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
