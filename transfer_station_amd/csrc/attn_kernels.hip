@@ -143,6 +143,18 @@ __device__ __forceinline__ u32x4 load_vt8(const uint16_t *base, int d, int key, 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// acc + the sum of the 8 bf16 values of v, two per v_dot2c_f32_bf16 against (1, 1): products
+// with 1 are exact, and the sums are fp32.
+__device__ __forceinline__ float sum_bf16x8(bf16x8 v, float acc) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    const u32x4 u = __builtin_bit_cast(u32x4, v);
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u[j]), one, acc, false);
+    return acc;
+}
+
 __device__ __forceinline__ bf16x8 join_tr(s16x4 lo, s16x4 hi) {
     typedef __attribute__((ext_vector_type(8))) short s16x8;
     s16x8 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -1715,6 +1727,13 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     }
 }
 
+// Row padding (floats) of the decode kernels' 4-wave merge area [4][16][DP + kMergePad]. Each
+// lane stores its O^T registers (rows r16 = lane % 16, columns 16db + 4grp .. +3) as 16 bytes;
+// with unpadded rows (DP = 64 or 128 floats: a multiple of the 64 four-byte banks) the 16 lanes
+// of a group hit the same 4 banks, a 16-way conflict (3.0 M conflict cycles per c2 decode
+// dispatch); 4 floats of padding move each row 4 banks on, so the 16 lanes cover all 64.
+constexpr int kMergePad = 4;
+
 // ------------------------------------------------------------------------------------------
 // Decode (split-K). One workgroup per (kv head u, split sp, 16-row block rb) serves up to 16 of
 // the M = g*Sq <= 64 query rows of that kv head from one read of its K/V range
@@ -1736,12 +1755,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float *__restrict__ pl, float *__restrict__ pacc, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nsplit, int kps, int nrb) {
     constexpr int VSTR = DP + 16;
+    // Rows 8..15 and 24..31 of a V tile (odd row-octets) are stored rotated by VROT elements:
+    // one 32-lane pass of a transposed read covers rows 8g .. 8g+3 and 8g+8 .. 8g+11, which any
+    // row stride that keeps 16-byte chunks aligned puts on the same banks (2 conflict cycles per
+    // read at DP = 128); rotated by half a 256-byte row they take the other 32 banks. At DP = 64
+    // no rotation within the 128-byte row separates them, and the 2-way conflict stays.
+    constexpr int VROT = (DP == 128) ? 64 : 0;
     constexpr int VNCH = 32 * DP / 8 / 64; // 16-byte chunks per lane per V tile
     constexpr int VTILE = 32 * VSTR;       // elements of one wave's V tile
     __shared__ __attribute__((aligned(16))) uint16_t Vw[4 * VTILE];
     __shared__ float red_m[4][16], red_l[4][16];
-    // The 4-wave merge reuses the V tiles' memory as float [4][16][DP].
-    static_assert(4 * 16 * DP * 4 <= 4 * VTILE * 2, "merge area must fit in the V tiles");
+    // The 4-wave merge reuses the V tiles' memory as float [4][16][DP + 4] (kMergePad).
+    static_assert(4 * 16 * (DP + kMergePad) * 4 <= 4 * VTILE * 2,
+                  "merge area must fit in the V tiles");
 
     // Block = (kv head u, split sp, row block rb): rows 16rb .. 16rb+15 of the kv head's M rows.
     // Row blocks of one (u, sp) are consecutive logical ids, kept on one XCD so that they share
@@ -1812,7 +1838,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             for (int r = 0; r < VNCH; ++r) {
                 const int cidx = lane + 64 * r;
                 const int row = cidx / (DP / 8), col = (cidx % (DP / 8)) * 8;
-                *reinterpret_cast<u32x4 *>(&vt[row * VSTR + col]) = vv[r];
+                const int colr = (col + VROT * ((row >> 3) & 1)) & (DP - 1);
+                *reinterpret_cast<u32x4 *>(&vt[row * VSTR + colr]) = vv[r];
             }
         }
         f32x4 s[2];
@@ -1862,11 +1889,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
                 o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv[db]), pk, o[db], 0, 0, 0);
         } else {
             lds_wave_fence(); // this tile's V is in LDS before the transposed reads
-            const uint16_t *vb = &vt[(8 * grp + (r16 >> 2)) * VSTR + 4 * (r16 & 3)];
+            // rows of this lane's reads: 8grp + r16/4 and 4 on, in row-octet grp
+            const int vrot = VROT * (grp & 1);
+            const uint16_t *vb0 = &vt[(8 * grp + (r16 >> 2)) * VSTR + 4 * (r16 & 3)];
 #pragma unroll
             for (int db = 0; db < DP / 16; ++db) {
+                // column 16db + 4(r16 % 4) + vrot, modulo DP (db * 16 < DP - VROT: no wrap)
+                const uint16_t *vb = vb0 + db * 16 + ((db * 16 < DP - VROT) ? vrot : -vrot);
                 const bf16x8 a =
-                    join_tr(lds_read_tr(vb + db * 16), lds_read_tr(vb + db * 16 + 4 * VSTR));
+                    join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * VSTR));
                 o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pk, o[db], 0, 0, 0);
             }
         }
@@ -1876,7 +1907,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
     // Merge the 4 waves: O^T register (db, i) of this lane holds d = 16db + 4grp + i, row r16.
     __syncthreads();
-    float *om = reinterpret_cast<float *>(Vw); // [4][16][DP]
+    float *om = reinterpret_cast<float *>(Vw); // [4][16][DP + kMergePad]
     if (grp == 0) {
         red_m[w][r16] = m_run;
         red_l[w][r16] = l_run;
@@ -1885,7 +1916,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int db = 0; db < DP / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            om[(w * 16 + r16) * DP + db * 16 + 4 * grp + i] = o[db][i];
+            om[(w * 16 + r16) * (DP + kMergePad) + db * 16 + 4 * grp + i] = o[db][i];
     __syncthreads();
     for (int idx = tid; idx < Mb * D; idx += 256) {
         const int r = idx / D, d = idx - r * D;
@@ -1898,7 +1929,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
             const float wgt = fast_exp2((red_m[ww][r] - muse) * c);
-            acc += wgt * om[(ww * 16 + r) * DP + d];
+            acc += wgt * om[(ww * 16 + r) * (DP + kMergePad) + d];
             lsum += wgt * red_l[ww][r];
         }
         const int hr = u * g + (row0 + r) / Sq, qr = (row0 + r) % Sq;
@@ -1944,7 +1975,8 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
     constexpr int TILE = RQ * GK;    // elements of one tile
     __shared__ __attribute__((aligned(1024))) uint16_t Vt[2][TILE];
     __shared__ float red_m[4][16], red_l[4][16];
-    static_assert(4 * 16 * DP * 4 <= 2 * TILE * 2, "merge area must fit in the V^T tiles");
+    static_assert(4 * 16 * (DP + kMergePad) * 4 <= 2 * TILE * 2,
+                  "merge area must fit in the V^T tiles");
 
     const int g = Hq / Hkv, M = g * Sq;
     // The grid is Hkv * nsplit * nrb workgroups.
@@ -2129,7 +2161,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
 
     // Merge the 4 waves (as attn_decode_kernel): O^T register (db, i) holds d = 16db + 4grp + i.
     __syncthreads();
-    float *om = reinterpret_cast<float *>(&Vt[0][0]); // [4][16][DP]
+    float *om = reinterpret_cast<float *>(&Vt[0][0]); // [4][16][DP + kMergePad]
     if (grp == 0) {
         red_m[w][r16] = m_run;
         red_l[w][r16] = l_run;
@@ -2138,7 +2170,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
     for (int db = 0; db < DP / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            om[(w * 16 + r16) * DP + db * 16 + 4 * grp + i] = o[db][i];
+            om[(w * 16 + r16) * (DP + kMergePad) + db * 16 + 4 * grp + i] = o[db][i];
     __syncthreads();
     for (int idx = tid; idx < Mb * D; idx += 256) {
         const int r = idx / D, d = idx - r * D;
@@ -2151,7 +2183,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
             const float wgt = fast_exp2((red_m[ww][r] - muse) * c);
-            acc += wgt * om[(ww * 16 + r) * DP + d];
+            acc += wgt * om[(ww * 16 + r) * (DP + kMergePad) + d];
             lsum += wgt * red_l[ww][r];
         }
         const int hr = u * g + (row0 + r) / Sq, qr = (row0 + r) % Sq;

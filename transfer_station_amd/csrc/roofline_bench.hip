@@ -8,6 +8,8 @@
 //   roofline_bench copy <MiB>      one float4 copy of <MiB> MiB (PMC calibration: known bytes)
 //   roofline_bench read <MiB>      streaming read of <MiB> MiB, ordinary and non-temporal loads
 //   roofline_bench mix             the headline prefill kernel's per-tile instruction mix, with parts removed
+//   roofline_bench ldsprobe        the split-K decode kernel's LDS access patterns, one kernel each
+//                                  (run under rocprofv3 --pmc SQ_LDS_BANK_CONFLICT for conflicts)
 //
 // Grid shapes are fixed at launch and every index is bounded by the buffer sizes below.
 #include <hip/hip_runtime.h>
@@ -763,6 +765,81 @@ static double run_split(int nv) {
     return best;
 }
 
+// LDS bank-conflict probes: the split-K decode kernel's per-wave LDS access patterns, one kernel
+// per pattern, so that rocprofv3 --pmc SQ_LDS_BANK_CONFLICT attributes the counts to each:
+//   P = 0: the V tile stores, 8 ds_write_b128 per wave writing 32 key rows of 256 bytes at a
+//          row stride of RS bytes (lane + 64 r -> row / 16, 16-byte chunk % 16);
+//   P = 1: the transposed V reads, 16 ds_read_b64_tr_b16 per wave, lane (g = lane / 16,
+//          r = lane % 16) at row 8g + r / 4 (and 4 rows on), bytes 8 (r % 4) + 32 db;
+//   P = 2: the row exchanges, __shfl_xor by 16 and by 32.
+// Each wave owns 32 rows of RS bytes; every address stays inside them.
+template <int P, int RS>
+__global__ __launch_bounds__(256) void lds_probe(unsigned *out, int iters) {
+    constexpr int RE = RS / 2; // row stride in elements
+    __shared__ __attribute__((aligned(16))) unsigned short tile[4 * 32 * RE];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int i = threadIdx.x; i < 4 * 32 * RE; i += 256)
+        tile[i] = (unsigned short)i;
+    __syncthreads();
+    unsigned short *vt = &tile[w * 32 * RE];
+    unsigned acc = lane;
+    for (int it = 0; it < iters; ++it) {
+        if constexpr (P == 0) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int cidx = lane + 64 * r, row = cidx / 16, col = (cidx % 16) * 8;
+                const u32x4_t v = {(unsigned)it, (unsigned)r, acc, 0u};
+                *reinterpret_cast<u32x4_t *>(&vt[row * RE + col]) = v;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        } else if constexpr (P == 1) {
+            const int g = lane >> 4, r = lane & 15;
+            const unsigned short *vb = &vt[(8 * g + (r >> 2)) * RE + 4 * (r & 3)];
+#pragma unroll
+            for (int db = 0; db < 8; ++db) {
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_t *)(vb + db * 16));
+                const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4_t *)(vb + db * 16 + 4 * RE));
+                acc += (unsigned)(lo[0] ^ hi[3]);
+            }
+        } else {
+            float x = (float)acc;
+            x += __shfl_xor(x, 16);
+            x += __shfl_xor(x, 32);
+            acc = (unsigned)x;
+        }
+    }
+    out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+// Runs each LDS probe once over 4 workgroups per CU; returns the probes' ms (rocprofv3 reads
+// the counters).
+static void run_lds_probes(double *ms) {
+    int cus = 0;
+    CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+    const int blocks = cus * 4, iters = 2000;
+    unsigned *out;
+    CHECK(hipMalloc(&out, (size_t)blocks * 256 * sizeof(unsigned)));
+    hipEvent_t a, b;
+    CHECK(hipEventCreate(&a));
+    CHECK(hipEventCreate(&b));
+    for (int k = 0; k < 5; ++k) {
+        CHECK(hipEventRecord(a, 0));
+        switch (k) {
+        case 0: hipLaunchKernelGGL((lds_probe<0, 288>), dim3(blocks), dim3(256), 0, 0, out, iters); break;
+        case 1: hipLaunchKernelGGL((lds_probe<1, 288>), dim3(blocks), dim3(256), 0, 0, out, iters); break;
+        case 2: hipLaunchKernelGGL((lds_probe<2, 288>), dim3(blocks), dim3(256), 0, 0, out, iters); break;
+        case 3: hipLaunchKernelGGL((lds_probe<0, 256>), dim3(blocks), dim3(256), 0, 0, out, iters); break;
+        default: hipLaunchKernelGGL((lds_probe<1, 256>), dim3(blocks), dim3(256), 0, 0, out, iters); break;
+        }
+        CHECK(hipGetLastError());
+        CHECK(hipEventRecord(b, 0));
+        ms[k] = time_ms(a, b);
+    }
+    CHECK(hipFree(out));
+}
+
 static double run_valu(bool exp) {
     int cus = 0, clk_khz = 0;
     CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
@@ -987,6 +1064,12 @@ int main(int argc, char **argv) {
                    "\"shader_clocks_per_tile\": %.0f, \"mfma_clocks_per_tile\": 4096}\n",
                    e.name, tf, g, cpt);
         }
+    } else if (!strcmp(mode, "ldsprobe")) {
+        double ms[5];
+        run_lds_probes(ms);
+        printf("{\"lds_probe_ms\": {\"v_store_b128_rs288\": %.3f, \"v_read_tr_rs288\": %.3f, "
+               "\"shfl_xor_16_32\": %.3f, \"v_store_b128_rs256\": %.3f, \"v_read_tr_rs256\": %.3f}}\n",
+               ms[0], ms[1], ms[2], ms[3], ms[4]);
     } else if (!strcmp(mode, "valu")) {
         printf("{\"exp_chain_steps_per_simd_clk\": %.4f, \"fma_per_simd_clk\": %.4f}\n",
                run_valu(true), run_valu(false));
@@ -1003,7 +1086,7 @@ int main(int argc, char **argv) {
                "\"copy_gbps\": %.1f, \"read_gbps\": %.1f, \"stream_mib\": %zu}\n",
                m32, m16, mr, cp, rd, mib);
     } else {
-        fprintf(stderr, "usage: %s [all|mfma|clock|split|coissue|chain|lds|mix|valu|copy MiB|read MiB]\n", argv[0]);
+        fprintf(stderr, "usage: %s [all|mfma|clock|split|coissue|chain|lds|mix|ldsprobe|valu|copy MiB|read MiB]\n", argv[0]);
         return 2;
     }
     return 0;
