@@ -14,8 +14,9 @@
  * How this harness differs from the reference's, on purpose:
  *   - Inputs live in device memory. A pool of copies at distinct addresses, together at
  *     least twice the last-level cache, makes every timed call read cold inputs
- *     (flash.c:982-991). Copy 0 holds the LCG data; the rest are device-side duplicates, since
- *     what makes a call cold is its addresses, not its values. The pool is labelled "hbm".
+ *     (flash.c:982-991). Copy 0 holds the LCG data (with --normal, seeded N(0,1) data); the
+ *     rest are device-side duplicates, since what makes a call cold is its addresses, not its
+ *     values. The pool is labelled "hbm".
  *   - --llc-mb 0 sizes the pool from the device: its L2 plus the MI355X's 256 MiB Infinity
  *     Cache (which the runtime does not report).
  *   - Times are device times from HIP events around batches of back-to-back calls. One fused
@@ -56,15 +57,17 @@
 struct config {
     int suite_long, prepack_v, sweep, pick_selftest, help, no_softmax;
     int bk, iters, warmup, llc_mib;
+    long normal_seed; /* -1: the reference's LCG data */
     double min_secs;
     const char *shape_text;
 };
 
 static struct config cfg = {
-    .bk = ATTN_BK_DEFAULT, .iters = 0, .warmup = 3, .llc_mib = 512, .min_secs = 0.5,
+    .bk = ATTN_BK_DEFAULT, .iters = 0, .warmup = 3, .llc_mib = 512, .normal_seed = -1,
+    .min_secs = 0.5,
 };
 
-enum opt_kind { OPT_SWITCH, OPT_INT, OPT_REAL, OPT_TEXT };
+enum opt_kind { OPT_SWITCH, OPT_INT, OPT_LONG, OPT_REAL, OPT_TEXT };
 
 struct opt {
     const char *name;
@@ -90,6 +93,9 @@ static const struct opt options[] = {
     {"--warmup", OPT_INT, &cfg.warmup, "N", "untimed calls before the timed ones (default 3)"},
     {"--bench-secs", OPT_REAL, &cfg.min_secs, "S",
      "without --iters: keep timing until S seconds and at least 3 calls (default 0.5)"},
+    {"--normal", OPT_LONG, &cfg.normal_seed, "SEED",
+     "instead of the reference's LCG data, seeded N(0,1) bf16 Q, K, V drawn from one counter\n"
+     "stream in that order (the benchmark's generator; bench.py's config 3 data: SEED 305419899)"},
     {"--llc-mb", OPT_INT, &cfg.llc_mib, "N",
      "cache size in MiB that the input pool must exceed twice over (default 512;\n"
      "0: the device's L2 plus its 256 MiB Infinity Cache)"},
@@ -177,6 +183,13 @@ static int parse_args(int argc, char **argv) {
                 return 0;
             }
             *(int *)o->target = (int)v;
+        } else if (o->kind == OPT_LONG) {
+            long v;
+            if (!whole_int(val, &v) || v < 0) {
+                printf("flash_cli: option %s wants a non-negative integer, got '%s'\n", o->name, val);
+                return 0;
+            }
+            *(long *)o->target = v;
         } else {
             char *end = NULL;
             double v = strtod(val, &end);
@@ -322,12 +335,20 @@ static int bench_open(struct bench *b, const struct shape *s, int bk, size_t cac
     b->hv = malloc(b->nkv * 2);
     if (!b->hq || !b->hk || !b->hv)
         return -1;
-    /* The reference's data: its LCG restarted at 0x12345678 for every case (flash.c:1030),
-     * drawn Q, then K, then V. */
-    uint32_t state = 0x12345678u;
-    attn_synth_lcg_bf16(&state, b->hq, b->nq);
-    attn_synth_lcg_bf16(&state, b->hk, b->nkv);
-    attn_synth_lcg_bf16(&state, b->hv, b->nkv);
+    if (cfg.normal_seed >= 0) {
+        /* N(0,1) bf16, one counter stream: Q, then K, then V */
+        const uint64_t seed = (uint64_t)cfg.normal_seed;
+        attn_synth_normal_bf16(b->hq, b->nq, seed, 0, 1.0);
+        attn_synth_normal_bf16(b->hk, b->nkv, seed, b->nq, 1.0);
+        attn_synth_normal_bf16(b->hv, b->nkv, seed, b->nq + b->nkv, 1.0);
+    } else {
+        /* The reference's data: its LCG restarted at 0x12345678 for every case (flash.c:1030),
+         * drawn Q, then K, then V. */
+        uint32_t state = 0x12345678u;
+        attn_synth_lcg_bf16(&state, b->hq, b->nq);
+        attn_synth_lcg_bf16(&state, b->hk, b->nkv);
+        attn_synth_lcg_bf16(&state, b->hv, b->nkv);
+    }
 
     b->bytes[SLOT_Q] = b->nq * 2;
     b->bytes[SLOT_K] = b->bytes[SLOT_V] = b->bytes[SLOT_VT] = b->nkv * 2;
@@ -387,7 +408,10 @@ static void call_pack(const struct bench *b, int i) {
 
 /* Mean device seconds per call of `op`: warmup calls, then batches (doubling up to MAX_BATCH)
  * between two HIP events, until --iters calls or, without it, MIN_TIMED_CALLS calls and
- * --bench-secs of wall time. */
+ * --bench-secs of wall time. The warmup runs --warmup calls and, when --warmup is above 0, at
+ * least WARMUP_MIN_S seconds: after the host-side setup the GPU is idle, and its clock takes
+ * about 40 ms of work to settle (bench.py --ramp measures it), which a few calls do not cover. */
+#define WARMUP_MIN_S 0.2
 struct timing {
     double per_call;
     int calls;
@@ -397,8 +421,13 @@ static struct timing measure(const struct bench *b, void (*op)(const struct benc
     void *start = NULL, *stop = NULL;
     must(attn_dev_event_create(&start), "event");
     must(attn_dev_event_create(&stop), "event");
-    for (int i = 0; i < cfg.warmup; i++)
+    const double w0 = wall_seconds();
+    for (int i = 0; i < cfg.warmup || (cfg.warmup > 0 && wall_seconds() - w0 < WARMUP_MIN_S);
+         i++) {
         op(b, i);
+        if (i % 16 == 15)
+            must(attn_dev_synchronize(), "warmup"); /* the wall clock then tracks the GPU */
+    }
     must(attn_dev_synchronize(), "warmup");
     struct timing t = {0.0, 0};
     double device_s = 0.0;

@@ -52,6 +52,7 @@ def run(cli, *args, timeout=300):
     (["--iters", "-5"], "must be >= 0"),
     (["--warmup", "-1"], "must be >= 0"),
     (["--llc-mb", "-16"], "must be >= 0"),
+    (["--normal", "-1"], "wants a non-negative integer"),
     (["--bench-secs", "fast"], "wants a number"),
     (["--frobnicate"], "unrecognised option '--frobnicate'"),
     (["--no-softmax"], "--no-softmax is rejected"),
@@ -82,8 +83,9 @@ def case_lines(out):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("extra", [[], ["--prepack-v"], ["--bk", "16"], ["--bk", "4096"]],
-                         ids=["default", "prepack-v", "bk16", "bk4096"])
+@pytest.mark.parametrize("extra", [[], ["--prepack-v"], ["--bk", "16"], ["--bk", "4096"],
+                                   ["--normal", "7"]],
+                         ids=["default", "prepack-v", "bk16", "bk4096", "normal-data"])
 def test_default_suite(cli, extra):
     r = run(cli, "--bench-secs", "0.05", "--llc-mb", "16", *extra)
     assert r.returncode == 0, r.stdout
