@@ -4,7 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 One step = one attn_flash call (one fused kernel launch) over the headline workload,
-BASELINE config 3 at 4k: GQA prefill B=4, Hq=32, Hkv=8, D=128, Sq=Sk=4096, non-causal,
+Benchmark configuration c3 at 4k: GQA prefill B=4, Hq=32, Hkv=8, D=128, Sq=Sk=4096, non-causal,
 bf16 Q/K/V ~ N(0,1) (synthetic, seeded), fp32 O. Inputs are resident in HBM before timing;
 each timed call rotates through a pool of input copies larger than 2x the 256 MiB Infinity
 Cache, so every call streams from HBM (the reference's DDR-cold rule, flash.c:982-991).
@@ -12,7 +12,7 @@ Cache, so every call streams from HBM (the reference's DDR-cold rule, flash.c:98
 Prints ONE JSON line on stdout (diagnostics go to stderr). `value` is TFLOP/s of useful
 work 4*B*Hq*Sq*Sk*D per step over the wall-clock of the timed steps; `roofline.achieved`
 is the same work over the kernel's average duration from HIP events on its stream. The
-other BASELINE configurations (decode GB/s, 1k/2k prefill, MQA, ragged) are reported
+other benchmark configurations (decode GB/s, 1k/2k prefill, MQA, ragged) are reported
 under "extra". The CPU baseline is the oracle (the reference's scalar fp32 attn_ref,
 restated in C) timed on a bounded spread-row sample of the same workload.
 """
@@ -337,8 +337,8 @@ def main():
         # ---- config 3 at 1k/2k, config 4, config 5, config 1 --------------------------------
         # (name, B, Hq, Hkv, Sq, Sk, D, sigma_q, seed index, bks, causal); qwen3_4k_causal is the
         # reference's own --long case (flash.c:1312-1314), causal, useful flops only; the last
-        # one is a serving shape outside the BASELINE configs (a 512-query chunk over 8192 keys,
-        # batch 1: few query tiles, so the key range is split over workgroups and merged).
+        # one is a serving shape outside the benchmark configurations (a 512-query chunk over
+        # 8192 keys, batch 1: few query tiles, so the key range is split over workgroups and merged).
         # bk does not select the GPU's key tile (it is fixed by D), so every bk runs one kernel:
         # a case with several bk values is timed once, at the first, and the outputs at the
         # other bk values are checked to be bit-identical to it.

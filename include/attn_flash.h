@@ -92,6 +92,15 @@ void pack_v_full(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D);
 void attn_flash_noalloc(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O, int Hq,
                         int Hkv, int Sq, int Sk, int D, int causal, int bk, int v_prepacked);
 
+/* Kernel plan of an attn_flash call (no counterpart in the reference: introspection for tests
+ * and integrators, who can see which kernels a shape takes on the current device). Runs
+ * attn_flash's host-side choice for these arguments and, instead of launching, writes one line
+ * per kernel the call would launch -- "name<template arguments> [notes] grid=x block=n" -- into
+ * buf, NUL-terminated. Returns the length written, or -1 when buf is too small. Reads and writes
+ * no device memory; the argument checks are attn_flash's (tensors and scratch aside). */
+int attn_flash_plan(int Hq, int Hkv, int Sq, int Sk, int D, int causal, int bk, int v_prepacked,
+                    char *buf, size_t len);
+
 /* Stream selection for the calling thread (no counterpart in the reference, which has
  * no device). `stream` is a hipStream_t; NULL selects the null stream. */
 void attn_flash_set_stream(void *stream);

@@ -109,7 +109,7 @@ void orc_lcg_bf16(uint32_t *state, uint16_t *out, size_t n) {
     *state = s;
 }
 
-/* ---- seeded N(0, sigma^2) data mode (this build's spec for the BASELINE configs) ------
+/* ---- seeded N(0, sigma^2) data mode (the data of the benchmark configurations) ------
  * Element c of a stream (Q at counters [0,nq), K at [nq,nq+nk), V after) takes two
  * counter-based splitmix64 outputs x_j = mix(seed + (2c+j+1)*0x9E3779B97F4A7C15),
  * j = 0,1; U1 = ((x_0>>11)+0.5)*2^-53 in (0,1), U2 = (x_1>>11)*2^-53 in [0,1);

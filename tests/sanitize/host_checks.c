@@ -74,8 +74,34 @@ struct last_call {
 };
 static struct last_call lc;
 
+/* attn_flash_plan: while a plan is recorded the real launchers write kernel lines instead of
+ * launching; these stand-ins then touch no partials (the scratch is a stand-in address). */
+static char *g_plan;
+static size_t g_plan_len, g_plan_pos;
+void attn_hip_plan_begin(char *buf, size_t len) {
+    g_plan = buf;
+    g_plan_len = len;
+    g_plan_pos = 0;
+    buf[0] = '\0';
+}
+long attn_hip_plan_end(void) {
+    g_plan = NULL;
+    return (long)g_plan_pos;
+}
+static void plan_line(const char *what) {
+    const size_t n = strlen(what);
+    if (g_plan_pos + n + 2 <= g_plan_len) {
+        memcpy(g_plan + g_plan_pos, what, n);
+        g_plan_pos += n;
+        g_plan[g_plan_pos++] = '\n';
+        g_plan[g_plan_pos] = '\0';
+    }
+}
+
 /* Writes slots [0, n) of the (m, l, acc[D]) partial arrays, as a kernel storing n partials. */
 static void touch_partials(float *pm, float *pl, float *pacc, long n, int D) {
+    if (g_plan)
+        return;
     for (long s = 0; s < n; s++) {
         pm[s] = -1.0f;
         pl[s] = 1.0f;
@@ -90,6 +116,8 @@ int attn_hip_launch_prefill(const uint16_t *Q, const uint16_t *K, const uint16_t
     (void)Q, (void)K, (void)V, (void)O, (void)Sq, (void)Sk, (void)causal, (void)vec, (void)vt,
         (void)c, (void)stream;
     lc.prefill_calls++;
+    if (g_plan)
+        plan_line("prefill");
     CHECK(Hq % Hkv == 0 && D <= dp && (dp == 64 || dp == 128 || dp == 256), "prefill args");
     CHECK(slots == SLOTS, "prefill slot capacity %ld", slots);
     /* A causal split may use any of the slots: write all of them. */
@@ -103,6 +131,8 @@ int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, const uint16_t 
                            int kps, int nrb, void *stream) {
     (void)Q, (void)K, (void)V, (void)O, (void)causal, (void)vec, (void)vt, (void)c, (void)stream;
     lc.decode_calls++;
+    if (g_plan)
+        plan_line("decode");
     lc.nsplit = nsplit;
     lc.kps = kps;
     lc.nrb = nrb;
@@ -128,6 +158,10 @@ int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, f
     lc.merge_calls++;
     lc.merge_rows = rows;
     CHECK(nsplit == lc.nsplit, "merge nsplit %d, decode nsplit %d", nsplit, lc.nsplit);
+    if (g_plan) {
+        plan_line("merge");
+        return 0;
+    }
     /* Read every partial the merge reads. */
     double acc = 0.0;
     const long n = (long)rows * nsplit;
@@ -302,8 +336,20 @@ static void check_oracle(void) {
     CHECK(s1 == s2 && memcmp(buf, buf2, sizeof buf) == 0, "LCG generators agree");
 }
 
+/* attn_flash_plan runs the host-side choice with stand-in pointers and touches no memory: a
+ * prefill, a split decode (with its merge) and a short buffer. */
+static void check_plan(void) {
+    char buf[256];
+    int n = attn_flash_plan(128, 32, 4096, 4096, 128, 0, 128, 0, buf, sizeof buf);
+    CHECK(n > 0 && strcmp(buf, "prefill\n") == 0, "plan of a prefill: %d '%s'", n, buf);
+    n = attn_flash_plan(32, 8, 1, 32768, 128, 0, 128, 0, buf, sizeof buf);
+    CHECK(n > 0 && strcmp(buf, "decode\nmerge\n") == 0, "plan of a split decode: %d '%s'", n,
+          buf);
+}
+
 int main(void) {
     check_scratch_sizes();
+    check_plan();
     check_pick_bk();
     check_attention_calls();
     check_oracle();

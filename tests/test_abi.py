@@ -166,3 +166,18 @@ def test_library_missing_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.lib()
+
+
+def test_parse_plan_lines():
+    text = ("attn_decode_kernel<128, false, true, false, false> nsplit=64 nrb=1 grid=512 block=256\n"
+            "attn_mergew_kernel nsplit=64 grid=8 block=256\n"
+            "attn_merge2_kernel grid=8,2,1 block=256\n")
+    assert ts.parse_plan(text) == [
+        ("attn_decode_kernel<128, false, true, false, false>", "nsplit=64 nrb=1", "512", 256),
+        ("attn_mergew_kernel", "nsplit=64", "8", 256),
+        ("attn_merge2_kernel", "", "8,2,1", 256)]
+
+
+def test_plan_checks_arguments_before_any_device_call():
+    r = _run_py("import transfer_station_amd as ts; ts.attn_flash_plan(4, 4, 8, 8, 64, 0, 100)")
+    assert r.returncode == -signal.SIGABRT and "bk" in r.stderr

@@ -86,7 +86,7 @@ def test_golden_fixtures_direct():
         assert err <= 8e-3, m["name"]
 
 
-# ---- the BASELINE configurations ---------------------------------------------------------------
+# ---- the benchmark configurations c1-c5 --------------------------------------------------------
 def test_c1_mha_256(oracle):
     Q, K, V = ts.synth_normal_qkv(4, 4, 256, 256, 64, SEED0 + 1)
     check(oracle, "c1 MHA", Q, K, V, 4, 4, 256, 256, 64, 0, 128)
@@ -619,6 +619,57 @@ def test_forced_wave_counts(waves, kh):
                        text=True, timeout=240)
     say(r.stdout[-2000:] + r.stderr[-2000:])
     assert r.returncode == 0 and r.stdout.strip().endswith("OK")
+
+
+# ---- which kernels each configuration takes (attn_flash_plan) --------------------------------------
+# (label, Hq, Hkv, Sq, Sk, D, causal, v_prepacked, [(kernel, required note), ...] in launch order):
+# the benchmark configurations c1-c5, the reference's Qwen3 --long case, a chunked-prefill
+# serving shape and a long-context split decode, as the host-side choice takes them on a
+# 256-CU MI355X.
+PLANS = [
+    ("c1 MHA 256", 4, 4, 256, 256, 64, 0, 0,
+     [("attn_prefill_fast_kernel<64, 128, 4, false, false, false>", "nsplit=1")]),
+    ("c2 GQA decode", 2048, 512, 1, 4096, 128, 0, 0,
+     [("attn_decode_kernel<128, false, true, false, true>", "nsplit=1")]),
+    ("c2 GQA decode, V^T", 2048, 512, 1, 4096, 128, 0, 1,
+     [("attn_decode_vt_kernel<128, false, true>", "nsplit=1")]),
+    ("c3 1k", 128, 32, 1024, 1024, 128, 0, 0, [("attn_prefill_persist_kernel<128, false>", "units=512")]),
+    ("c3 2k", 128, 32, 2048, 2048, 128, 0, 0, [("attn_prefill_persist_kernel<128, false>", "units=1024")]),
+    ("c3 4k", 128, 32, 4096, 4096, 128, 0, 0, [("attn_prefill_persist_kernel<128, false>", "units=2048")]),
+    ("c3 4k causal", 128, 32, 4096, 4096, 128, 1, 0,
+     [("attn_prefill_persist_kernel<128, true>", "units=1024")]),
+    ("c3 4k, V^T", 128, 32, 4096, 4096, 128, 0, 1,
+     [("attn_prefill_fast_kernel<128, 128, 8, false, true, false>", "nsplit=1")]),
+    ("c4 MQA 2k", 128, 8, 2048, 2048, 128, 0, 0, [("attn_prefill_persist_kernel<128, false>", "units=1024")]),
+    ("c5 ragged D 64", 48, 12, 1000, 4000, 64, 0, 0,
+     [("attn_prefill_fast_kernel<64, 128, 4, false, false, false>", "hsplit=16"),
+      ("attn_merge2_kernel", "")]),
+    ("Qwen3 4k causal", 16, 8, 4096, 4096, 128, 1, 0,
+     [("attn_prefill_fast_kernel<128, 128, 8, true, false, true>", "nsplit=1")]),
+    ("chunked 512 over 8192, causal", 32, 8, 512, 8192, 128, 1, 0,
+     [("attn_prefill_fast_kernel<128, 128, 8, true, false, true>", "nsplit=2"),
+      ("attn_merge2_kernel", "")]),
+    ("batch-1 decode 32k", 32, 8, 1, 32768, 128, 0, 0,
+     [("attn_decode_kernel<128, false, true, false, false>", "nsplit=64"),
+      ("attn_mergew_kernel", "nsplit=64")]),
+]
+
+
+@pytest.mark.parametrize("case", PLANS, ids=[c[0] for c in PLANS])
+def test_kernel_plan(case):
+    """attn_flash_plan records, without launching, the kernels a call takes; a change in the
+    host-side choice shows here as a failure rather than only as a slower bench line. The
+    persistent prefill takes one workgroup per CU."""
+    if ts.device_info()["cus"] != 256:
+        pytest.skip("the kernel choice is pinned for a 256-CU MI355X")
+    label, Hq, Hkv, Sq, Sk, D, causal, vt, want = case
+    plan = ts.attn_flash_plan(Hq, Hkv, Sq, Sk, D, causal, 128, vt)
+    say("plan %s: %s" % (label, plan))
+    assert [k for k, _, _, _ in plan] == [k for k, _ in want], label
+    for (k, notes, grid, block), (_, need) in zip(plan, want):
+        assert need in notes.split() or need == "", (label, k, notes)
+        if k.startswith("attn_prefill_persist_kernel"):
+            assert grid == "256" and block == 512, (label, grid, block)
 
 
 _PERSIST_SCRIPT = r"""

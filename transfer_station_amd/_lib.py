@@ -19,6 +19,7 @@ _SIGNATURES = {
     "pack_v_full": (None, [_c.c_void_p, _c.c_void_p, _c.c_int, _c.c_int, _c.c_int]),
     "attn_flash_noalloc": (None, [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_void_p] +
                            [_c.c_int] * 8),
+    "attn_flash_plan": (_c.c_int, [_c.c_int] * 8 + [_c.c_char_p, _c.c_size_t]),
     "attn_flash_set_stream": (None, [_c.c_void_p]),
     "attn_flash_get_stream": (_c.c_void_p, []),
     # include/attn_devutil.h

@@ -110,6 +110,33 @@ def attn_flash_noalloc(Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, bk, v_prepacked=0
                              int(Sk), int(D), int(bool(causal)), int(bk), int(v_prepacked))
 
 
+def attn_flash_plan(Hq, Hkv, Sq, Sk, D, causal, bk=ATTN_BK_DEFAULT, v_prepacked=0):
+    """The kernels an attn_flash call with these arguments launches on the current device, as
+    a list of (kernel, notes, grid, block) from the library's host-side choice; nothing is
+    launched."""
+    buf = ctypes.create_string_buffer(4096)
+    n = lib().attn_flash_plan(int(Hq), int(Hkv), int(Sq), int(Sk), int(D), int(bool(causal)),
+                              int(bk), int(v_prepacked), buf, len(buf))
+    if n < 0:
+        raise RuntimeError("attn_flash_plan: the plan does not fit the buffer")
+    return parse_plan(buf.value.decode())
+
+
+def parse_plan(text):
+    """Lines "name[<template arguments>] [notes] grid=x[,y,z] block=n" -> a list of
+    (name, notes, grid, block)."""
+    out = []
+    for line in text.splitlines():
+        head, _, tail = line.partition(" grid=")
+        grid, _, block = tail.partition(" block=")
+        # the kernel name runs to its closing '>' when it has template arguments, else to the
+        # first space; the notes follow it
+        first = head.split(" ", 1)[0]
+        cut = head.index(">") + 1 if "<" in first else len(first)
+        out.append((head[:cut], head[cut:].strip(), grid, int(block)))
+    return out
+
+
 def pack_v_full(V, Vp, Hkv, Sk, D):
     lib().pack_v_full(_addr(V), _addr(Vp), int(Hkv), int(Sk), int(D))
 

@@ -29,6 +29,8 @@ int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc, f
                           int D, int nsplit, float c, int Sq, void *stream);
 int attn_hip_launch_pack_v(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D, void *stream);
 int attn_hip_device_cus(void);
+void attn_hip_plan_begin(char *buf, size_t len);
+long attn_hip_plan_end(void);
 int attn_hip_static_scratch(void **ptr, size_t *bytes);
 
 /* ---- device scratch layout ---------------------------------------------------------------
@@ -286,6 +288,23 @@ void attn_flash_noalloc(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
     if (bytes < attn_layout(NULL, D, NULL) || ((uintptr_t)scratch % ATTN_SCRATCH_ALIGN) != 0)
         attn_fail(who, "static scratch is smaller than its layout or misaligned");
     attn_run(who, Q, K, V, O, Hq, Hkv, Sq, Sk, D, causal, scratch, v_prepacked, NULL);
+}
+
+/* The host-side kernel choice of attn_flash for these arguments, recorded instead of launched:
+ * no device memory is read or written. Stand-in pointers are 256-aligned and non-NULL, as a
+ * caller's tensors and scratch are, so every alignment- and scratch-dependent choice is the one
+ * attn_flash makes. */
+int attn_flash_plan(int Hq, int Hkv, int Sq, int Sk, int D, int causal, int bk, int v_prepacked,
+                    char *buf, size_t len) {
+    static const char *who = "attn_flash_plan";
+    const uint16_t *p = (const uint16_t *)(uintptr_t)ATTN_SCRATCH_ALIGN;
+    attn_check_args(who, p, p, p, (const float *)p, Hq, Hkv, Sq, Sk, D, bk);
+    if (!buf || len == 0)
+        attn_fail(who, "buf must be non-NULL and len above 0");
+    attn_hip_plan_begin(buf, len);
+    attn_run(who, p, p, p, (float *)p, Hq, Hkv, Sq, Sk, D, causal, (void *)p, v_prepacked, NULL);
+    const long n = attn_hip_plan_end();
+    return n < 0 || n > 0x7fffffffL ? -1 : (int)n;
 }
 
 void pack_v_full(const uint16_t *V, uint16_t *Vp, int Hkv, int Sk, int D) {

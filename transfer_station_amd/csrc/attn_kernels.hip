@@ -24,8 +24,11 @@
 //                                          vector path / any shape)
 // VT selects a pre-transposed V ([Hkv][D][Sk], pack_v_full's layout).
 #include <hip/hip_runtime.h>
+#include <stdarg.h>
 #include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <atomic>
@@ -2454,6 +2457,42 @@ template <typename F> hipError_t with_flag(bool b, F &&f) {
     return b ? f(std::true_type{}) : f(std::false_type{});
 }
 
+// Plan recording (attn_flash_plan): while t_plan is set on the calling thread, each launch
+// site writes one line per kernel it would launch ("name<template arguments> grid=x[,y,z]
+// block=n", then the site's notes) into the caller's buffer instead of launching.
+struct plan_buf {
+    char *buf;
+    size_t len, pos;
+    bool truncated;
+};
+thread_local plan_buf *t_plan = nullptr;
+const char *tf(bool b) { return b ? "true" : "false"; }
+
+__attribute__((format(printf, 3, 4))) void plan_note(dim3 g, dim3 b, const char *fmt, ...) {
+    plan_buf *p = t_plan;
+    char line[256];
+    va_list ap;
+    va_start(ap, fmt);
+    int n = vsnprintf(line, sizeof line, fmt, ap);
+    va_end(ap);
+    if (n < 0)
+        n = 0;
+    size_t used = (size_t)n < sizeof line ? (size_t)n : sizeof line - 1;
+    int m = (g.y > 1 || g.z > 1)
+                ? snprintf(line + used, sizeof line - used, " grid=%u,%u,%u block=%u\n", g.x, g.y,
+                           g.z, b.x * b.y * b.z)
+                : snprintf(line + used, sizeof line - used, " grid=%u block=%u\n", g.x,
+                           b.x * b.y * b.z);
+    used += (m > 0 && (size_t)m < sizeof line - used) ? (size_t)m : 0;
+    if (p->pos + used + 1 > p->len) {
+        p->truncated = true;
+        return;
+    }
+    memcpy(p->buf + p->pos, line, used);
+    p->pos += used;
+    p->buf[p->pos] = '\0';
+}
+
 template <int DP, int KT, bool CAUSAL, bool VEC, bool VT>
 hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t *V, float *O,
                             int Hq, int Hkv, int Sq, int Sk, int D, float c, hipStream_t st) {
@@ -2461,8 +2500,12 @@ hipError_t launch_prefill_t(const uint16_t *Q, const uint16_t *K, const uint16_t
     const long nblk = (long)Hq * nqt;
     if (nblk <= 0 || nblk > 0x7fffffffL)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_kernel<DP, KT, CAUSAL, VEC, VT>), dim3((unsigned)nblk),
-                       dim3(256), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt);
+    if (t_plan)
+        plan_note(dim3((unsigned)nblk), dim3(256), "attn_prefill_kernel<%d, %d, %s, %s, %s>", DP,
+                  KT, tf(CAUSAL), tf(VEC), tf(VT));
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<DP, KT, CAUSAL, VEC, VT>), dim3((unsigned)nblk),
+                           dim3(256), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt);
     return hipGetLastError();
 }
 
@@ -2476,15 +2519,26 @@ hipError_t launch_merge(const float *pm, const float *pl, const float *pacc, flo
         while (lpr < 64 && 4 * lpr < D)
             lpr *= 2;
         const long rpw = 256 / lpr; // rows per workgroup
-        hipLaunchKernelGGL(attn_merge2_kernel, dim3((unsigned)((rows + rpw - 1) / rpw)), dim3(256),
-                           0, st, pm, pl, pacc, O, rows, D, c, rph, q_off, Sq, lpr);
+        if (t_plan)
+            plan_note(dim3((unsigned)((rows + rpw - 1) / rpw)), dim3(256), "attn_merge2_kernel");
+        else
+            hipLaunchKernelGGL(attn_merge2_kernel, dim3((unsigned)((rows + rpw - 1) / rpw)),
+                               dim3(256), 0, st, pm, pl, pacc, O, rows, D, c, rph, q_off, Sq, lpr);
     }
-    else if (nsplit <= kMergeWaveMaxSplit)
-        hipLaunchKernelGGL(attn_mergew_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
-                           pm, pl, pacc, O, rows, D, nsplit, c, rph, q_off, Sq);
-    else if (nsplit <= kMergeMaxSplit && D <= 256)
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, pm, pl, pacc,
-                           O, D, nsplit, c, rph, q_off, Sq);
+    else if (nsplit <= kMergeWaveMaxSplit) {
+        if (t_plan)
+            plan_note(dim3((unsigned)((rows + 3) / 4)), dim3(256), "attn_mergew_kernel nsplit=%d",
+                      nsplit);
+        else
+            hipLaunchKernelGGL(attn_mergew_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                               st, pm, pl, pacc, O, rows, D, nsplit, c, rph, q_off, Sq);
+    } else if (nsplit <= kMergeMaxSplit && D <= 256) {
+        if (t_plan)
+            plan_note(dim3((unsigned)rows), dim3(256), "attn_merge_kernel nsplit=%d", nsplit);
+        else
+            hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)rows), dim3(256), 0, st, pm, pl,
+                               pacc, O, D, nsplit, c, rph, q_off, Sq);
+    }
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2649,9 +2703,17 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                                        nsplit == 1 &&
                                                        prefill_wg_per_cu(DP, KT, NW) == 2,
                                                    nblk);
-    hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT, KH>), dim3((unsigned)nblk),
-                       dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, split_first, pm,
-                       pl, pacc, prows, pack, pair_r, prefill_pipe(), nsplit, (int)nblk, hsplit);
+    if (t_plan)
+        plan_note(dim3((unsigned)nblk), dim3(NW * 64),
+                  "attn_prefill_fast_kernel<%d, %d, %d, %s, %s, %s> nsplit=%d split_first=%d "
+                  "hsplit=%d pack=%d pair=%d",
+                  DP, KT, NW, tf(CAUSAL), tf(VT), tf(KH), nsplit, split_first, hsplit, pack,
+                  pair_r);
+    else
+        hipLaunchKernelGGL((attn_prefill_fast_kernel<DP, KT, NW, CAUSAL, VT, KH>),
+                           dim3((unsigned)nblk), dim3(NW * 64), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk,
+                           D, c, nqt, split_first, pm, pl, pacc, prows, pack, pair_r,
+                           prefill_pipe(), nsplit, (int)nblk, hsplit);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
@@ -2793,8 +2855,13 @@ hipError_t launch_prefill_persist(const uint16_t *Q, const uint16_t *K, const ui
     const int nwg = device_cus() / 8 * 8;
     if (nunits <= 0 || nunits > 0x3fffffffL || nwg <= 0)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_prefill_persist_kernel<DP, CAUSAL>), dim3((unsigned)nwg), dim3(512),
-                       0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nunits, nwg);
+    if (t_plan)
+        plan_note(dim3((unsigned)nwg), dim3(512), "attn_prefill_persist_kernel<%d, %s> units=%ld",
+                  DP, tf(CAUSAL), nunits);
+    else
+        hipLaunchKernelGGL((attn_prefill_persist_kernel<DP, CAUSAL>), dim3((unsigned)nwg),
+                           dim3(512), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nunits,
+                           nwg);
     return hipGetLastError();
 }
 
@@ -2925,10 +2992,15 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
         if (vt && vec && decode_vt_staged() && (long)D * Sk * 2 < 0x7fffffffL)
             return with_flag(causal != 0, [&](auto CA) {
                 return with_flag(ntl, [&](auto NT) {
-                    hipLaunchKernelGGL(
-                        (attn_decode_vt_kernel<DP, decltype(CA)::value, decltype(NT)::value>),
-                        dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq, Hkv,
-                        Sq, Sk, D, c, nsplit, kps, nrb);
+                    if (t_plan)
+                        plan_note(dim3((unsigned)nblk), dim3(256),
+                                  "attn_decode_vt_kernel<%d, %s, %s> nsplit=%d nrb=%d", DP,
+                                  tf(decltype(CA)::value), tf(decltype(NT)::value), nsplit, nrb);
+                    else
+                        hipLaunchKernelGGL(
+                            (attn_decode_vt_kernel<DP, decltype(CA)::value, decltype(NT)::value>),
+                            dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq,
+                            Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
                     return hipGetLastError();
                 });
             });
@@ -2936,11 +3008,17 @@ hipError_t launch_decode_d(const uint16_t *Q, const uint16_t *K, const uint16_t 
         return with_flag(vec != 0, [&](auto VE) {
             return with_flag(vt != 0, [&](auto VTF) {
                 return with_flag(ntl, [&](auto NT) {
-                    hipLaunchKernelGGL(
-                        (attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
-                                            decltype(VTF)::value, decltype(NT)::value>),
-                        dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq, Hkv,
-                        Sq, Sk, D, c, nsplit, kps, nrb);
+                    if (t_plan)
+                        plan_note(dim3((unsigned)nblk), dim3(256),
+                                  "attn_decode_kernel<%d, %s, %s, %s, %s> nsplit=%d nrb=%d", DP,
+                                  tf(decltype(CA)::value), tf(decltype(VE)::value),
+                                  tf(decltype(VTF)::value), tf(decltype(NT)::value), nsplit, nrb);
+                    else
+                        hipLaunchKernelGGL(
+                            (attn_decode_kernel<DP, decltype(CA)::value, decltype(VE)::value,
+                                                decltype(VTF)::value, decltype(NT)::value>),
+                            dim3((unsigned)nblk), dim3(256), 0, st, Q, K, V, O, pm, pl, pacc, Hq,
+                            Hkv, Sq, Sk, D, c, nsplit, kps, nrb);
                     return hipGetLastError();
                 });
             });
@@ -2999,6 +3077,23 @@ extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, cons
 
 // Compute units of the current device, for the host layer's kernel choice.
 extern "C" int attn_hip_device_cus(void) { return device_cus(); }
+
+// Plan recording for attn_flash_plan: between begin and end, the launchers of the calling
+// thread write kernel lines into buf (NUL-terminated) instead of launching. end returns the
+// length written, or -1 if buf was too small for every line.
+namespace {
+thread_local plan_buf t_plan_state;
+}
+extern "C" void attn_hip_plan_begin(char *buf, size_t len) {
+    t_plan_state = plan_buf{buf, len, 0, false};
+    if (len > 0)
+        buf[0] = '\0';
+    t_plan = &t_plan_state;
+}
+extern "C" long attn_hip_plan_end(void) {
+    t_plan = nullptr;
+    return t_plan_state.truncated ? -1L : (long)t_plan_state.pos;
+}
 
 extern "C" int attn_hip_launch_merge(const float *pm, const float *pl, const float *pacc,
                                      float *O, int rows, int D, int nsplit, float c, int Sq,
