@@ -421,7 +421,7 @@ def test_score_jumps_between_key_tiles(oracle, Hq, Hkv, Sq, Sk, D, causal):
     Q = oracle.f32_to_bf16(q).reshape(-1)
     K = oracle.f32_to_bf16(k).reshape(-1)
     V = ts.synth_normal_bf16(Hkv * Sk * D, 32, 0)
-    persist = Hq * ((Sq + 255) // 256) >= 512
+    persist = ts.attn_flash_plan(Hq, Hkv, Sq, Sk, D, causal)[0][0].startswith("attn_prefill_persist")
     O = check(oracle, "score jumps", Q, K, V, Hq, Hkv, Sq, Sk, D, causal,
               ref_cap=8 if persist else 0)
     Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, causal, prepack_v=True)
