@@ -32,6 +32,25 @@ HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E (published)
 SEED0 = 0x12345678
 INFINITY_CACHE = 256 << 20
 
+# VALU-issue floor of the online softmax, per score and SIMD: one v_fma_f32 (s*c - m*c), one
+# v_exp_f32, one v_add_f32 (the row sum of the fp32 p) and half a v_cvt_pk_bf16_f32 (P to bf16),
+# with packed FP32 off. A wave64 VALU instruction takes 4 cycles on a 16-lane SIMD; v_exp_f32
+# about twice that (roofline_bench valu: 4.4 cycles per fma, 11.8 per exp + add step). That is
+# 18 cycles per 64 scores. 1024 SIMDs at the 2.4 GHz rating.
+VALU_CYCLES_PER_SCORE = (4 + 8 + 4 + 2) / 64.0
+SIMDS, CLOCK_HZ = 1024, 2.4e9
+
+
+def bounds(flops, scores, kernel_ms):
+    """The MFMA and VALU-issue floors of a prefill (ms) and the kernel's fraction of the higher
+    one, the roofline that binds: D = 64 has half the MFMA work per score of D = 128 and the same
+    softmax, so its VALU floor passes its MFMA floor."""
+    mfma_ms = flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
+    valu_ms = scores * VALU_CYCLES_PER_SCORE / (SIMDS * CLOCK_HZ) * 1e3
+    bound = "valu" if valu_ms > mfma_ms else "mfma"
+    return {"mfma_floor_ms": mfma_ms, "valu_floor_ms": valu_ms, "bound": bound,
+            "bound_frac": max(mfma_ms, valu_ms) / kernel_ms}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -293,7 +312,8 @@ def main():
         extra["c3_gqa_prefill_4k_causal"] = {
             "kernel_ms": k, "TFLOP_s": cflops / (k * 1e-3) / 1e12,
             "mfma_frac": cflops / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-            "flop_note": "4*D per unmasked (q,k) pair", "parity": pc}
+            "flop_note": "4*D per unmasked (q,k) pair", "parity": pc,
+            **bounds(cflops, cflops / (4.0 * D), k)}
         log("c3 4k causal:", extra["c3_gqa_prefill_4k_causal"])
         # ---- the same workload with a pre-packed V^T (v_prepacked=1) ---------------------------
         pk_ms = time_pack_v(ts, bufs, B, Hkv, S, D)
@@ -358,6 +378,7 @@ def main():
             w, k = time_calls(ts, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, cz, bks[0], sc, 20, 3)
             res = {"bk": bks[0], "kernel_ms": k, "TFLOP_s": fl / (k * 1e-3) / 1e12,
                    "mfma_frac": fl / (k * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+            res.update(bounds(fl, Bc * Hqc * pairs, k))
             res["parity"] = parity(ts, o, cb, Bc, Hqc, Hkvc, Sq, Sk, Dc, cz, 8, nthreads)
             if len(bks) > 1:
                 q, kk, v, out, _ = cb[0]
@@ -403,6 +424,8 @@ def main():
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                      "kernel_ms": round(kern_ms, 4), "flop_per_launch": flops,
+                     "valu_issue_floor_ms": round(bounds(flops, flops / (4.0 * D),
+                                                         kern_ms)["valu_floor_ms"], 4),
                      "measured_peaks": peaks,
                      "frac_of_measured_random_operand_peak":
                          (round(achieved / peaks["mfma32x32x16_bf16_random_operands_tflops"], 4)
