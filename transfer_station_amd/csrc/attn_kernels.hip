@@ -15,6 +15,9 @@
 //   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT,KH>  MFMA prefill for D % 8 == 0, D <= DP in
 //                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows,
 //                                          or (KH) 8 waves over 128 rows on key-tile halves
+//   attn_prefill_persist_kernel<DP,CAUSAL> the same tile code at D <= 128, one 8-wave workgroup
+//                                          per CU running its 256-row items back to back
+//                                          (causal: pairs of a heavy and a light query tile)
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T, staged in LDS 512 keys at a time
@@ -145,18 +148,6 @@ __device__ __forceinline__ u32x4 load_vt8(const uint16_t *base, int d, int key, 
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-// acc + the sum of the 8 bf16 values of v, two per v_dot2c_f32_bf16 against (1, 1): products
-// with 1 are exact, and the sums are fp32.
-__device__ __forceinline__ float sum_bf16x8(bf16x8 v, float acc) {
-    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-    const u32x4 u = __builtin_bit_cast(u32x4, v);
-    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, u[j]), one, acc, false);
-    return acc;
-}
 
 __device__ __forceinline__ bf16x8 join_tr(s16x4 lo, s16x4 hi) {
     typedef __attribute__((ext_vector_type(8))) short s16x8;
@@ -1266,12 +1257,13 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill, persistent (non-causal, D % 8 == 0, D <= DP = 128, at least two rounds of 8-wave
-// workgroups). The fast kernel runs one (query head, 256-row tile) item per workgroup, and each
-// item pays a fixed cost outside its key loop: all CUs load Q and the first key tile at once
-// (an HBM burst), store O at once, and wait for the next workgroup's dispatch. Here one 8-wave
-// workgroup per CU runs its items back to back, and the key-tile pipeline continues across
-// them:
+// Prefill, persistent (D % 8 == 0, D <= DP = 128, at least two rounds of 8-wave workgroups;
+// causal grids as pairs of a heavy and a light query tile, whose key tiles add up to the same
+// count for every pair). The fast kernel runs one (query head, 256-row tile) item per
+// workgroup, and each item pays a fixed cost outside its key loop: all CUs load Q and the first
+// key tile at once (an HBM burst), store O at once, and wait for the next workgroup's dispatch.
+// Here one 8-wave workgroup per CU runs its items back to back, and the key-tile pipeline
+// continues across them:
 //   * the next item's first K/V tile is the last tile's ordinary LDS-DMA prefetch;
 //   * the next item's Q (registers) is loaded during the last tile, after its S^T, so it lands
 //     under the softmax and P.V (the last tile takes the row max, so no recompute needs the
@@ -1285,9 +1277,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // [xb, xb + nx) (kv-head-major, as xcd_remap deals them) and its i-th workgroup takes
 // xb + i, xb + i + R, ... (R workgroups per XCD), so each round of an XCD shares one kv head's
 // K/V in its L2 as before. The tile code is the fast kernel's (8 waves, 32 rows each, 128-key
-// tiles, lazy rescale with the sum test), without causal masks, for row-major V only: a V^T
-// variant needs 4 more offset registers for its DMA, spills them, and its spill reloads then
-// wait for the DMA in flight (measured 0.5-2.6% slower than the V^T fast kernel on c3 and c4).
+// tiles, lazy rescale with the sum test; causal masks compared against immediates), for
+// row-major V only: a V^T variant needs 4 more offset registers for its DMA, spills them, and
+// its spill reloads then wait for the DMA in flight (measured 0.5-2.6% slower than the V^T fast
+// kernel on c3 and c4).
 // ------------------------------------------------------------------------------------------
 // s_waitcnt operand (gfx9 encoding) that waits until at most n vector memory operations of
 // the wave are in flight, with no wait on expcnt or lgkmcnt.
@@ -1746,7 +1739,7 @@ constexpr int kMergePad = 4;
 //   S^T[key][row] = K . Q^T  (A = K rows loaded from global straight into the operand layout)
 //   O^T[d][row]  += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from a wave-private LDS tile)
 // The 4 waves merge in LDS; the workgroup writes O directly (nsplit == 1) or one partial
-// (m, l, acc[D]) per row into the caller's scratch for attn_merge_kernel.
+// (m, l, acc[D]) per row into the caller's scratch for the merge kernels (launch_merge).
 // VT: V arrives as V^T ([Hkv][D][Sk]); the V^T operand (row d, 8 consecutive keys per lane) is
 // then loaded from global memory straight into its register layout, like K, with no LDS tile.
 // NTL: K and V are loaded non-temporally (decode_nt_loads decides).
@@ -2596,7 +2589,7 @@ static int prefill_pipe() {
 // Key split of a prefill grid that fills at most half of one round of resident workgroups
 // (few query tiles, long key ranges: chunked prefill, small batches): each query tile's key
 // tiles are cut into nsplit near-equal parts, run as separate workgroups that write partials
-// (m, l, acc) to the scratch, and attn_merge_kernel combines them. nsplit fills one round,
+// (m, l, acc) to the scratch, and a merge kernel (launch_merge) combines them. nsplit fills one round,
 // keeps at least kSplitMinTiles key tiles per part and fits the scratch's partial slots.
 // Causal grids take it only when the keys before the query block (Sk - Sq) are at least as many
 // as the queries, so that query tiles attend similar key counts; triangular causal grids keep
@@ -2814,8 +2807,8 @@ static int prefill_kt_forced() {
     return forced;
 }
 
-// The persistent prefill (attn_prefill_persist_kernel) for non-causal 8-wave grids of at least
-// two rounds: ATTN_PREFILL_PERSIST=0 (read once) turns it off for tuning sweeps.
+// The persistent prefill (attn_prefill_persist_kernel) for 8-wave grids of at least two rounds,
+// non-causal or causal: ATTN_PREFILL_PERSIST=0 (read once) turns it off for tuning sweeps.
 static int prefill_persist() {
     static int env = -1;
     if (env < 0) {
