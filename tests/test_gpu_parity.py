@@ -879,3 +879,20 @@ def test_random_shapes_wide(oracle, case):
     i, Hq, Hkv, Sq, Sk, D, causal, bk = case
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 2000 + i)
     check(oracle, "wide random %d" % i, Q, K, V, Hq, Hkv, Sq, Sk, D, causal, bk, ref_cap=4)
+
+
+def test_persistent_phase_stamps():
+    """The stamps build of the persistent prefill (transfer_station_amd/phases.py) records, per
+    workgroup, times that never run backwards, whose span is the kernel's duration, at the
+    product library's speed within 15%."""
+    from transfer_station_amd import phases
+    s, st = phases.timeline(128, 32, 1024, 1024, 128, 0)
+    say("phases c3 1k: %s" % s)
+    busy = st[:, 0] > 0
+    assert busy.sum() == s["workgroups"] > 0
+    used = [0, 1] + [2 + i for i in range(8)] + [st.shape[1] - 1]  # two items per workgroup here
+    seq = st[busy][:, used].astype(np.int64)
+    assert (np.diff(seq, axis=1) >= 0).all()
+    ms = s["kernel_ms_product"]
+    assert 0.5 * ms <= s["span_us"] * 1e-3 <= 1.5 * ms
+    assert abs(s["kernel_ms_stamps_build"] / ms - 1) <= 0.15

@@ -19,6 +19,9 @@ INCLUDE = os.path.join(ROOT, "include")
 LIBDIR = os.path.join(PKG, "lib")
 OBJDIR = os.path.join(PKG, "_build")
 LIBNAME = "libattn_flash.so"
+# The same library with the persistent prefill's phase stamps compiled in (ATTN_PHASE_STAMPS=1),
+# for transfer_station_amd/phases.py only; nothing else loads it.
+STAMPS_LIBNAME = "libattn_flash_stamps.so"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["attn_kernels.hip"]
@@ -51,6 +54,10 @@ def lib_path():
     return os.path.join(LIBDIR, LIBNAME)
 
 
+def stamps_lib_path():
+    return os.path.join(LIBDIR, STAMPS_LIBNAME)
+
+
 def tool_path(name):
     return os.path.join(LIBDIR, name)
 
@@ -62,14 +69,20 @@ def build(verbose=False, jobs=8):
     os.makedirs(OBJDIR, exist_ok=True)
     cmds = []
     objs = []
+    stamp_objs = []
     for s in HIP_SOURCES:
         o = os.path.join(OBJDIR, s + ".o")
         cmds.append([hipcc] + HIPCC_FLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
         objs.append(o)
+        o = os.path.join(OBJDIR, s + ".stamps.o")
+        cmds.append([hipcc] + HIPCC_FLAGS + ["-DATTN_PHASE_STAMPS=1", "-c", os.path.join(CSRC, s),
+                                             "-o", o])
+        stamp_objs.append(o)
     for s in C_SOURCES:
         o = os.path.join(OBJDIR, s + ".o")
         cmds.append(["gcc"] + CC_FLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
         objs.append(o)
+        stamp_objs.append(o)
     for exe, src in TOOL_SOURCES.items():
         cmds.append([hipcc] + HIPCC_FLAGS + [os.path.join(CSRC, src), "-o",
                                              os.path.join(LIBDIR, exe)])
@@ -77,11 +90,12 @@ def build(verbose=False, jobs=8):
         for out in ex.map(_run, cmds):
             if out and verbose:
                 print(out)
-    tmp = lib_path() + ".tmp"
-    _run(["g++", "-shared", "-o", tmp] + objs +
-         ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-fopenmp", "-lm",
-          "-Wl,-rpath," + os.path.join(ROCM, "lib")])
-    os.replace(tmp, lib_path())
+    for path, parts in ((lib_path(), objs), (stamps_lib_path(), stamp_objs)):
+        tmp = path + ".tmp"
+        _run(["g++", "-shared", "-o", tmp] + parts +
+             ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-fopenmp", "-lm",
+              "-Wl,-rpath," + os.path.join(ROCM, "lib")])
+        os.replace(tmp, path)
     return lib_path()
 
 

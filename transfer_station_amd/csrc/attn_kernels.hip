@@ -1286,6 +1286,33 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // the wave are in flight, with no wait on expcnt or lgkmcnt.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
+// Phase stamps of the persistent prefill, compiled in only with ATTN_PHASE_STAMPS=1 (the
+// separate libattn_flash_stamps.so that transfer_station_amd/phases.py loads; the product
+// library has none of this code). Wave 0 of each workgroup writes the 100 MHz real-time counter
+// into g_phase_stamps[workgroup][slot]: slot 0 at entry, 1 when the first item's Q and tile are
+// in, then four per item (its start, the end of its first tile, the start and the end of its
+// last tile) and the last slot once the final O stores have completed. Each stamp is one global
+// store of one lane, issued where no kernel wait depends on an exact count of outstanding
+// operations (before a tile's DMA, or before a full vmcnt(0) wait).
+#ifndef ATTN_PHASE_STAMPS
+#define ATTN_PHASE_STAMPS 0
+#endif
+constexpr int kPhaseSlots = 64;
+#if ATTN_PHASE_STAMPS
+__device__ unsigned long long *g_phase_stamps;
+#endif
+__device__ __forceinline__ void phase_stamp(int w, int lane, int slot) {
+#if ATTN_PHASE_STAMPS
+    if (w == 0 && slot < kPhaseSlots) {
+        const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+        if (lane == 0)
+            g_phase_stamps[(size_t)wg_id_x() * kPhaseSlots + slot] = t;
+    }
+#else
+    (void)w, (void)lane, (void)slot;
+#endif
+}
+
 template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
@@ -1601,6 +1628,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
     };
 
+    phase_stamp(w, lane, 0);
     {
         int h0, qt0;
         item(0, h0, qt0);
@@ -1609,6 +1637,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     }
     __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): Q and tile 0 of the first item
     __syncthreads();
+    phase_stamp(w, lane, 1);
     // One key tile kt of item k (kv head u, query tile qt): FIRST (kt = 0: the previous item's
     // O leaves, then the row max), LAST (kt = nkt - 1: the next item's tile 0 DMA and Q loads,
     // the mask, the row max) or neither (the sum test, a rare recompute). Item coordinates are
@@ -1709,18 +1738,26 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         const int nkt = __builtin_amdgcn_readfirstlane(nkt_of(qt));
         using B0 = std::integral_constant<int, 0>;
         using B1 = std::integral_constant<int, 1>;
+        phase_stamp(w, lane, 2 + 4 * k);
         step(u, qt, 0, k, B0{}, std::true_type{}, std::false_type{});
+        phase_stamp(w, lane, 3 + 4 * k);
         for (int kt = 1; kt + 1 < nkt; kt += 2) {
             step(u, qt, kt, k, B1{}, std::false_type{}, std::false_type{});
             step(u, qt, kt + 1, k, B0{}, std::false_type{}, std::false_type{});
         }
+        phase_stamp(w, lane, 4 + 4 * k);
         step(u, qt, nkt - 1, k, B1{}, std::false_type{}, std::true_type{});
+        phase_stamp(w, lane, 5 + 4 * k);
     }
     {
         int hl, qtl;
         item(nmine - 1, hl, qtl);
         store_o(hl, qtl, true);
     }
+#if ATTN_PHASE_STAMPS
+    __builtin_amdgcn_s_waitcnt(0x0F70); // the final O stores have completed
+    phase_stamp(w, lane, kPhaseSlots - 1);
+#endif
 }
 
 // Row padding (floats) of the decode kernels' 4-wave merge area [4][16][DP + kMergePad]. Each
@@ -3070,6 +3107,24 @@ extern "C" int attn_hip_launch_decode(const uint16_t *Q, const uint16_t *K, cons
 
 // Compute units of the current device, for the host layer's kernel choice.
 extern "C" int attn_hip_device_cus(void) { return device_cus(); }
+
+// Phase stamps (ATTN_PHASE_STAMPS builds only): the persistent prefill's later launches write
+// kPhaseSlots 64-bit stamps per workgroup into buf (device memory of at least workgroups *
+// slots * 8 bytes; NULL is not allowed). Returns the slot count, or -1 in a build without
+// stamps or when the pointer cannot be set.
+extern "C" int attn_hip_phase_stamps(void *buf) {
+#if ATTN_PHASE_STAMPS
+    if (!buf)
+        return -1;
+    unsigned long long *p = static_cast<unsigned long long *>(buf);
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_phase_stamps), &p, sizeof p) != hipSuccess)
+        return -1;
+    return kPhaseSlots;
+#else
+    (void)buf;
+    return -1;
+#endif
+}
 
 // Plan recording for attn_flash_plan: between begin and end, the launchers of the calling
 // thread write kernel lines into buf (NUL-terminated) instead of launching. end returns the
