@@ -1534,7 +1534,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
         }
     };
-    auto row_max = [&]() __attribute__((always_inline)) {
+    // fresh: an item's first tile, where l and o are still zero (o is then written, not
+    // accumulated, by that tile's P.V): m rises with no rescale to apply.
+    auto row_max = [&](auto fresh) __attribute__((always_inline)) {
         float mt[KT / 32];
 #pragma unroll
         for (int t = 0; t < KT / 32; ++t) {
@@ -1546,7 +1548,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         }
         const float mx = max_xor32(fmaxf(max3f(mt[0], mt[1], mt[2]), mt[3]));
         const bool raise = mx > m_run;
-        if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+        if constexpr (decltype(fresh)::value) {
+            m_run = raise ? mx : m_run;
+        } else if (__builtin_amdgcn_ballot_w64(raise) != 0) {
             const float mnew = raise ? mx : m_run;
             const float alpha = (mnew == m_run) ? 1.0f : fast_exp2((m_run - mnew) * c);
             l_run *= alpha;
@@ -1586,12 +1590,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         for (int db = 0; db < DP / 32; ++db)
             va[0][db] = vfrag(buf, 0, db);
     };
-    auto pv = [&](int buf) {
+    // fresh (an item's first tile): the first 16-key chunk starts the accumulators from zero.
+    auto pv = [&](int buf, auto fresh) {
 #pragma unroll
         for (int cc = 0; cc < KT / 16; ++cc) {
 #pragma unroll
             for (int db = 0; db < DP / 32; ++db) {
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], o[db], 0, 0,
+                const f32x16 acc =
+                    (decltype(fresh)::value && cc == 0) ? f32x16{} : o[db];
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], acc, 0, 0,
                                                                0);
                 if (cc + 1 < KT / 16)
                     va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
@@ -1668,12 +1675,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             item(k > 0 ? k - 1 : 0, hp, qtp);
             store_o(hp, qtp, k > 0);
             m_run = kNegInf;
-            l_run = 0.f;
-#pragma unroll
-            for (int db = 0; db < DP / 32; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    o[db][i] = 0.f;
+            l_run = 0.f; // o: written by this tile's P.V
         }
         int kbase = kt * KT;
         if constexpr (LAST || CAUSAL)
@@ -1699,7 +1701,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             if (!(CAUSAL && LAST) || kbase <= wmax) {
                 if (LAST || CAUSAL)
                     mask(kbase, qt);
-                row_max();
+                row_max(std::integral_constant<bool, FIRST>{});
                 l_run += exps();
             }
         } else {
@@ -1711,13 +1713,13 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
                 pv_first(buf);
                 if constexpr (CAUSAL)
                     mask(kbase, qt);
-                row_max();
+                row_max(std::false_type{});
                 psum = exps();
             }
             l_run += psum;
         }
         if (!(CAUSAL && LAST) || kbase <= wmax)
-            pv(buf);
+            pv(buf, std::integral_constant<bool, FIRST>{});
         if (!LAST || more) {
             // Wait for the next tile's DMA only: the O stores of tile 0 (NOST) are younger and
             // stay in flight. The last tile waits for everything (the next item's Q loads, issued
