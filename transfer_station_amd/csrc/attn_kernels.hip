@@ -461,6 +461,47 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, u
                                              voff, 0, IMM, AUX);
 }
 
+// Phase stamps of the prefill kernels, compiled in only with ATTN_PHASE_STAMPS=1 (the separate
+// libattn_flash_stamps.so that transfer_station_amd/phases.py loads; the product library has
+// none of this code). Wave 0 of each workgroup writes the 100 MHz real-time counter (and, in the
+// per-tile kernel, its CU and key-tile count) into g_phase_stamps[workgroup][slot]; the slots
+// of each kernel are listed where it writes them. Each stamp is one global store of one lane,
+// issued where no kernel wait depends on an exact count of outstanding operations (before a
+// tile's DMA, or before a full vmcnt(0) wait).
+#ifndef ATTN_PHASE_STAMPS
+#define ATTN_PHASE_STAMPS 0
+#endif
+constexpr int kPhaseSlots = 64;
+#if ATTN_PHASE_STAMPS
+__device__ unsigned long long *g_phase_stamps;
+#endif
+__device__ __forceinline__ void phase_value(int w, int lane, int slot, unsigned long long v) {
+#if ATTN_PHASE_STAMPS
+    if (w == 0 && lane == 0 && slot < kPhaseSlots)
+        g_phase_stamps[(size_t)wg_id_x() * kPhaseSlots + slot] = v;
+#else
+    (void)w, (void)lane, (void)slot, (void)v;
+#endif
+}
+__device__ __forceinline__ void phase_stamp(int w, int lane, int slot) {
+#if ATTN_PHASE_STAMPS
+    if (w == 0)
+        phase_value(w, lane, slot, __builtin_amdgcn_s_memrealtime());
+#else
+    (void)w, (void)lane, (void)slot;
+#endif
+}
+// The CU a workgroup runs on, as stamp data: XCC_ID above bits 15:8 of HW_ID (CU, SH and SE).
+__device__ __forceinline__ unsigned long long phase_cu() {
+#if ATTN_PHASE_STAMPS
+    const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_REG_HW_ID
+    const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20); // HW_REG_XCC_ID
+    return ((unsigned long long)(xcc & 15) << 8) | ((hw >> 8) & 0xff);
+#else
+    return 0;
+#endif
+}
+
 // Workgroups per CU the launch bounds ask for: 8 waves in all, unless the two K and V tiles
 // (8*KT*DP bytes of LDS) or the O and Q registers (DP > 128) allow only one workgroup.
 constexpr int prefill_wg_per_cu(int DP, int KT, int NW) {
@@ -565,6 +606,11 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 
     const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform: LDS-DMA bases in SGPRs
+    // Phase stamps (ATTN_PHASE_STAMPS builds): slot 0 at entry, 1 when Q and the first tile are
+    // in, 2 after the first tile, 3 after the last, 4 after the key halves' hand-over, the last
+    // slot once the O (or partial) stores have completed; slot 6 holds the CU, 7 the key tiles.
+    phase_stamp(w, lane, 0);
+    phase_value(w, lane, 6, phase_cu());
     const int wr = KH ? w % NR : w; // the wave's 32-row block of the workgroup's rows
     const int kh = KH ? w / NR : 0; // and its half of each key tile
     const int l32 = lane & 31, hi = lane >> 5;
@@ -1052,6 +1098,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                 qlds + l32 * DP + (((2 * kk + hi) ^ (l32 & QSWZ)) * 8)));
     }
     __syncthreads();
+    phase_stamp(w, lane, 1);
     // One key tile: the next tile's DMA, then Q.K^T, softmax and P.V of this one (FIRST: the
     // item's first tile, whose softmax takes the row max; ME: the tile may need the mask).
     auto step = [&](int kt, auto first, auto me) __attribute__((always_inline)) {
@@ -1093,6 +1140,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     };
     if (kt0 < kt1)
         step(kt0, std::true_type{}, std::true_type{});
+    phase_stamp(w, lane, 2);
     if constexpr (NW == 4 && DP > 64) {
         // Tiles from kt_e on may need the mask (keys past Sk, or past the causal limit of the
         // wave's first row); the loop before them has no mask code. Measured (same box) on the
@@ -1110,6 +1158,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         for (int kt = kt0 + 1; kt < kt1; ++kt)
             step(kt, std::false_type{}, std::true_type{});
     }
+    phase_stamp(w, lane, 3);
+    phase_value(w, lane, 7, (unsigned long long)(kt1 - kt0));
 
     if constexpr (KH) {
         // The second-half wave of each row block hands its (m, l, o) to the first-half wave
@@ -1153,6 +1203,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                     o[db][4 * i4 + j] = o[db][4 * i4 + j] * a1 + v[j] * a2;
             }
     }
+    phase_stamp(w, lane, 4);
     const float lt = l_run + __shfl_xor(l_run, 32);
     if (part >= 0 || nsplit > 1) {
         // Unnormalised partial of one key range: (m, l, acc) into slot (row, part) for the
@@ -1177,6 +1228,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                         *reinterpret_cast<f32x4 *>(prow + d) = v;
                 }
         }
+#if ATTN_PHASE_STAMPS
+        __builtin_amdgcn_s_waitcnt(0x0F70); // the partial stores have completed
+        phase_stamp(w, lane, kPhaseSlots - 1);
+#endif
         return;
     }
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
@@ -1254,6 +1309,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                     *reinterpret_cast<f32x4 *>(orow + d) = v;
             }
     }
+#if ATTN_PHASE_STAMPS
+    __builtin_amdgcn_s_waitcnt(0x0F70); // the O stores have completed
+    phase_stamp(w, lane, kPhaseSlots - 1);
+#endif
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1286,32 +1345,6 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // the wave are in flight, with no wait on expcnt or lgkmcnt.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-// Phase stamps of the persistent prefill, compiled in only with ATTN_PHASE_STAMPS=1 (the
-// separate libattn_flash_stamps.so that transfer_station_amd/phases.py loads; the product
-// library has none of this code). Wave 0 of each workgroup writes the 100 MHz real-time counter
-// into g_phase_stamps[workgroup][slot]: slot 0 at entry, 1 when the first item's Q and tile are
-// in, then four per item (its start, the end of its first tile, the start and the end of its
-// last tile) and the last slot once the final O stores have completed. Each stamp is one global
-// store of one lane, issued where no kernel wait depends on an exact count of outstanding
-// operations (before a tile's DMA, or before a full vmcnt(0) wait).
-#ifndef ATTN_PHASE_STAMPS
-#define ATTN_PHASE_STAMPS 0
-#endif
-constexpr int kPhaseSlots = 64;
-#if ATTN_PHASE_STAMPS
-__device__ unsigned long long *g_phase_stamps;
-#endif
-__device__ __forceinline__ void phase_stamp(int w, int lane, int slot) {
-#if ATTN_PHASE_STAMPS
-    if (w == 0 && slot < kPhaseSlots) {
-        const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-        if (lane == 0)
-            g_phase_stamps[(size_t)wg_id_x() * kPhaseSlots + slot] = t;
-    }
-#else
-    (void)w, (void)lane, (void)slot;
-#endif
-}
 
 template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
@@ -1635,6 +1668,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
     };
 
+    // Phase stamps (ATTN_PHASE_STAMPS builds): slot 0 at entry, 1 when the first item's Q and
+    // tile are in, four per item (its start, the end of its first tile, the start and the end of
+    // its last tile), the last slot once the final O stores have completed.
     phase_stamp(w, lane, 0);
     {
         int h0, qt0;

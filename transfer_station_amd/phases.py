@@ -108,6 +108,56 @@ def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal):
     }
 
 
+def summarize_tiles(stamps, slots):
+    """Phase times in microseconds of the per-tile prefill kernel (attn_prefill_fast_kernel: one
+    item per workgroup) from its stamps: slot 0 entry, 1 Q and first tile in, 2 after the first
+    tile, 3 after the last, 4 after the key halves' hand-over, slots - 1 stores complete; slot 6
+    the CU, slot 7 the key tiles."""
+    busy = np.nonzero(stamps[:, 0])[0]
+    base = int(stamps[busy, 0].min())
+    t = (stamps[busy].astype(np.int64) - base) * TICK_US
+    ntile = stamps[busy, 7].astype(np.int64)
+    cu = stamps[busy, 6].astype(np.int64)
+    end = t[:, slots - 1]
+    many = ntile > 1
+    per_tile = (t[many, 3] - t[many, 2]) / (ntile[many] - 1)
+
+    def stat(v):
+        v = np.asarray(v, dtype=np.float64)
+        if v.size == 0:
+            return None
+        return {"median": round(float(np.median(v)), 3), "min": round(float(v.min()), 3),
+                "max": round(float(v.max()), 3)}
+
+    # per CU: its workgroups in entry order; a CU idles from its last workgroup's end to the
+    # kernel's end, and between a workgroup's end and the next one's entry when it runs one at a
+    # time
+    span = float(end.max())
+    idle_end, wg_per_cu, gaps = [], [], []
+    for c in np.unique(cu):
+        m = cu == c
+        e0, e1 = t[m, 0], end[m]
+        order = np.argsort(e0)
+        wg_per_cu.append(int(m.sum()))
+        idle_end.append(span - float(e1.max()))
+        for a, b in zip(order[:-1], order[1:]):
+            if e0[b] >= e1[a]:
+                gaps.append(e0[b] - e1[a])
+    return {
+        "workgroups": int(busy.size), "cus": int(np.unique(cu).size),
+        "workgroups_per_cu": stat(wg_per_cu),
+        "entry_spread_us": round(float(t[:, 0].max()), 3),
+        "prologue_us": stat(t[:, 1] - t[:, 0]),
+        "first_tile_us": stat(t[:, 2] - t[:, 1]),
+        "key_tile_us": stat(per_tile),
+        "key_halves_handover_us": stat(t[:, 4] - t[:, 3]),
+        "epilogue_us": stat(end - t[:, 4]),
+        "gap_between_workgroups_us": stat(gaps),
+        "cu_idle_at_end_us": stat(idle_end),
+        "span_us": round(span, 3),
+    }
+
+
 def _stamps_lib():
     path = _build.stamps_lib_path()
     L = ctypes.CDLL(path)
@@ -131,8 +181,9 @@ def timeline(Hq, Hkv, Sq, Sk, D, causal=0, seed=0x12345678, warm_s=0.3):
     if L.attn_flash_plan(Hq, Hkv, Sq, Sk, D, causal, 128, 0, buf, len(buf)) < 0:
         raise RuntimeError("attn_flash_plan failed")
     plan = ts.parse_plan(buf.value.decode())
-    if len(plan) != 1 or not plan[0][0].startswith("attn_prefill_persist_kernel"):
-        raise ValueError("this shape does not run the persistent prefill: %s" % (plan,))
+    kernel = plan[0][0]
+    if not kernel.startswith(("attn_prefill_persist_kernel", "attn_prefill_fast_kernel")):
+        raise ValueError("this shape runs no stamped prefill kernel: %s" % (plan,))
     nwg = int(plan[0][2])
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, seed)
     bq, bk, bv = (ts.DeviceBuffer.from_array(a) for a in (Q, K, V))
@@ -164,8 +215,12 @@ def timeline(Hq, Hkv, Sq, Sk, D, causal=0, seed=0x12345678, warm_s=0.3):
         ms_product = run(lib.attn_flash, 20)
         run(L.attn_flash, 10)  # back to back: the stamps hold the last call's, warm
         stamps = st.download(np.uint64, nwg * slots).reshape(nwg, slots)
-        summary = summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal)
-        summary.update({"shape": [Hq, Hkv, Sq, Sk, D, causal],
+        if kernel.startswith("attn_prefill_persist_kernel"):
+            summary = summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal)
+        else:
+            summary = summarize_tiles(stamps, slots)
+        summary.update({"shape": [Hq, Hkv, Sq, Sk, D, causal], "kernel": kernel,
+                        "plan": [" ".join((k, n)).strip() for k, n, _, _ in plan],
                         "kernel_ms_stamps_build": round(ms_stamps, 4),
                         "kernel_ms_product": round(ms_product, 4)})
         return summary, stamps
@@ -174,16 +229,32 @@ def timeline(Hq, Hkv, Sq, Sk, D, causal=0, seed=0x12345678, warm_s=0.3):
             x.free()
 
 
+LABELS = (("cus", "CUs"), ("workgroups_per_cu", "workgroups per CU"),
+          ("entry_spread_us", "entry spread"),
+          ("prologue_us", "prologue (Q + first tile)"),
+          ("first_tile_us", "first key tile"),
+          ("key_tile_us", "key tile, steady"),
+          ("first_tile_extra_us", "first tile of an item, extra"),
+          ("last_tile_extra_us", "last tile of an item, extra"),
+          ("between_items_us", "between items"),
+          ("key_halves_handover_us", "key halves' hand-over"),
+          ("epilogue_us", "epilogue (O or partial stores)"),
+          ("tail_us", "tail (final O stores)"),
+          ("gap_between_workgroups_us", "gap between workgroups"),
+          ("cu_idle_at_end_us", "CU idle before the end"),
+          ("span_us", "span of the stamps"))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--shape", action="append",
                     help="Hq,Hkv,Sq,Sk,D[,causal] (repeatable; default: config 3 at 1k, 4k and "
-                         "4k causal)")
+                         "4k causal, the Qwen3 4k causal case and config 5)")
     ap.add_argument("--json", action="store_true", help="one JSON line per shape")
     args = ap.parse_args()
     shapes = [tuple(int(v) for v in s.split(",")) for s in args.shape] if args.shape else [
         (128, 32, 1024, 1024, 128, 0), (128, 32, 4096, 4096, 128, 0),
-        (128, 32, 4096, 4096, 128, 1)]
+        (128, 32, 4096, 4096, 128, 1), (16, 8, 4096, 4096, 128, 1), (48, 12, 1000, 4000, 64, 0)]
     for s in shapes:
         s = s + (0,) * (6 - len(s))
         summary, _ = timeline(*s)
@@ -194,18 +265,16 @@ def main():
               "%.4f ms), %d workgroups" % (s + (summary["kernel_ms_stamps_build"],
                                                 summary["kernel_ms_product"],
                                                 summary["workgroups"])))
-        print("  span of the stamps          %9.2f us" % summary["span_us"])
-        print("  entry spread                %9.2f us" % summary["entry_spread_us"])
-        for key, label in (("prologue_us", "prologue (Q + first tile)"),
-                           ("key_tile_us", "key tile, steady"),
-                           ("first_tile_extra_us", "first tile of an item, extra"),
-                           ("last_tile_extra_us", "last tile of an item, extra"),
-                           ("between_items_us", "between items"),
-                           ("tail_us", "tail (final O stores)")):
-            v = summary[key]
-            if v:
-                print("  %-27s %9.2f us  (min %.2f, max %.2f)" % (label, v["median"], v["min"],
-                                                                 v["max"]))
+        print("  plan: %s" % "; ".join(summary["plan"]))
+        for key, label in LABELS:
+            v = summary.get(key)
+            if v is None:
+                continue
+            if isinstance(v, dict):
+                print("  %-31s %9.2f  (min %.2f, max %.2f)" % (label, v["median"], v["min"],
+                                                              v["max"]))
+            else:
+                print("  %-31s %9.2f" % (label, v))
         print(flush=True)
 
 
