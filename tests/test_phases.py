@@ -52,3 +52,26 @@ def test_summary_of_synthetic_stamps():
     assert s["first_tile_extra_us"]["median"] == 1.0 and s["last_tile_extra_us"]["median"] == 2.0
     assert s["between_items_us"]["max"] == 0.0 and s["tail_us"]["median"] == 5.0
     assert abs(s["span_us"] - (1.5 + 4 + 2 * 27 + 5)) < 1e-9
+
+
+def test_key_halves_pairs_run_the_even_count_first():
+    # The key-halves variant runs one pair of 128-row tiles per workgroup, the tile of even
+    # key-tile count first, so that its LDS buffer order is fixed at compile time: with whole
+    # tiles (Sq % 128 == 0) every pair holds one tile of even and one of odd count.
+    for Hq, Hkv, Sq, Sk in ((16, 8, 4096, 4096), (32, 8, 2048, 2048), (64, 16, 1024, 1536),
+                            (64, 8, 1024, 1100), (128, 1, 512, 512)):
+        nqt, nwg = Sq // 128, 256
+        units = Hq * nqt // 2
+        assert units == nwg
+
+        def swap(qt):
+            return phases.key_tiles(qt, Sq, Sk, True, 128) % 2 == 1
+
+        got = collections.Counter()
+        for b in range(nwg):
+            qts = phases.items_of(b, nwg, units, Hq // Hkv, nqt, True, swap)
+            assert len(qts) == 2 and qts[0] + qts[1] == nqt - 1
+            n0, n1 = (phases.key_tiles(q, Sq, Sk, True, 128) for q in qts)
+            assert n0 % 2 == 0 and n1 % 2 == 1, (Hq, Sq, Sk, qts)
+            got.update(qts)
+        assert got == collections.Counter({qt: Hq for qt in range(nqt)})

@@ -15,9 +15,11 @@
 //   attn_prefill_fast_kernel<DP,KT,NW,CAUSAL,VT,KH>  MFMA prefill for D % 8 == 0, D <= DP in
 //                                          {64, 96, 128, 256}; one workgroup = NW waves x 32 rows,
 //                                          or (KH) 8 waves over 128 rows on key-tile halves
-//   attn_prefill_persist_kernel<DP,CAUSAL> the same tile code at D <= 128, one 8-wave workgroup
-//                                          per CU running its 256-row items back to back
-//                                          (causal: pairs of a heavy and a light query tile)
+//   attn_prefill_persist_kernel<DP,CAUSAL,KH> the same tile code at D <= 128, one 8-wave
+//                                          workgroup per CU running its 256-row items back to
+//                                          back (causal: pairs of a heavy and a light query
+//                                          tile), or (KH) one causal pair of 128-row items on
+//                                          key-tile halves
 //   attn_prefill_kernel<DP,KT,CAUSAL,VEC,VT> the same tiling for any D <= 256 and alignment
 //   attn_decode_kernel<DP,CAUSAL,VEC,VT>   split-K decode for g*Sq <= 64 rows per kv head
 //   attn_decode_vt_kernel<DP,CAUSAL>       the same from V^T, staged in LDS 512 keys at a time
@@ -471,7 +473,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t *lds, u
 #ifndef ATTN_PHASE_STAMPS
 #define ATTN_PHASE_STAMPS 0
 #endif
-constexpr int kPhaseSlots = 64;
+[[maybe_unused]] constexpr int kPhaseSlots = 64;
 #if ATTN_PHASE_STAMPS
 __device__ unsigned long long *g_phase_stamps;
 #endif
@@ -1340,19 +1342,28 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 // row-major V only: a V^T variant needs 4 more offset registers for its DMA, spills them, and
 // its spill reloads then wait for the DMA in flight (measured 0.5-2.6% slower than the V^T fast
 // kernel on c3 and c4).
+// KH (causal grids of exactly two 128-row query tiles per CU, where the fast kernel runs key
+// halves in two rounds): each workgroup runs one heavy/light pair of 128-row items, waves w and
+// w + 4 on the same 32 rows and the two 64-key halves of every tile. At each item's end the
+// two halves are merged through LDS (kh_put / kh_combine) and each wave stores half of its rows'
+// columns. A pair's key-tile counts add up to an odd number, so the item of even count runs
+// first: the buffer order stays a compile-time constant without a padding tile.
 // ------------------------------------------------------------------------------------------
 // s_waitcnt operand (gfx9 encoding) that waits until at most n vector memory operations of
 // the wave are in flight, with no wait on expcnt or lgkmcnt.
 constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
 
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool KH>
 __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, float *__restrict__ O, int Hq, int Hkv, int Sq, int Sk, int D,
     float c, int nqt, int nitems, int nwg) {
     static_assert(DP % 32 == 0 && DP <= 128, "tile shape");
-    constexpr int KT = 128, NW = 8, BQ = NW * 32;
+    static_assert(!KH || (CAUSAL && DP == 128), "key halves: causal pairs at DP = 128");
+    // KH: items of 128 rows, waves w and w + 4 (one SIMD) on the same 32 rows and the two
+    // 64-key halves of every tile (NR row blocks, KW keys per wave and tile).
+    constexpr int KT = 128, NW = 8, NR = KH ? NW / 2 : NW, KW = KH ? KT / 2 : KT, BQ = NR * 32;
     // One variable per tile buffer: the compiler tells LDS accesses apart by variable only, so
     // with the two buffers of an array it would make each tile's first reads wait for the DMA
     // of the next tile into the other buffer.
@@ -1362,6 +1373,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     __shared__ __attribute__((aligned(1024))) uint16_t Vs1[KT * DP];
     auto kbuf = [&](int buf) -> uint16_t * { return buf ? Ks1 : Ks0; }; // buf: a constant
     auto vbuf = [&](int buf) -> uint16_t * { return buf ? Vs1 : Vs0; };
+    __shared__ float kh_ml[KH ? NW * 128 : 1]; // KH: (m, l) of each lane, for its partner wave
 
     const int g = Hq / Hkv;
     const int b = wg_id_x(), x = b & 7, xi = b >> 3, R = nwg >> 3; // nwg % 8 == 0
@@ -1373,11 +1385,19 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const int nmine = CAUSAL ? 2 * nunits : nunits; // items of this workgroup
     if (nmine == 0)
         return;
-    // Item k of this workgroup: query head h and 256-row tile qt. Non-causal: the fast kernel's
-    // order (kv head, then tile, then the g heads of the group). Causal (nqt even): unit P is
-    // the pair of tiles nqt-1-p and p of one head (kv head, then p, then the head), whose key
-    // tiles add up to the same count for every p, run heavy first: each workgroup gets the
-    // same number of pairs and so the same work.
+    // Key tiles of an item: all of them, or (causal) those up to its last row's limit,
+    // Sk - Sq + its last row (Sk >= Sq). Even for every item (host), except with KH.
+    auto nkt_of = [&](int qt) {
+        if constexpr (CAUSAL)
+            return (Sk - Sq + min(Sq - 1, qt * BQ + BQ - 1)) / KT + 1;
+        return (Sk + KT - 1) / KT;
+    };
+    // Item k of this workgroup: query head h and query tile qt (BQ rows). Non-causal: the fast
+    // kernel's order (kv head, then tile, then the g heads of the group). Causal (nqt even):
+    // unit P is the pair of tiles nqt-1-p and p of one head (kv head, then p, then the head),
+    // whose key tiles add up to the same count for every p, run heavy first: each workgroup
+    // gets the same number of pairs and so the same work. KH (Sq % 128 == 0): the pair's
+    // counts add up to an odd number, and the tile of even count runs first.
     auto item = [&](int k, int &h, int &qt) {
         if constexpr (CAUSAL) {
             const int np = nqt >> 1;
@@ -1385,7 +1405,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             const int uu = P / (g * np);
             const int rr = P - uu * (g * np);
             const int pp = rr / g;
-            qt = __builtin_amdgcn_readfirstlane((k & 1) ? pp : nqt - 1 - pp);
+            const bool swap = KH && (nkt_of(nqt - 1 - pp) & 1);
+            qt = __builtin_amdgcn_readfirstlane(((k & 1) != swap) ? pp : nqt - 1 - pp);
             h = __builtin_amdgcn_readfirstlane(uu * g + (rr - pp * g));
         } else {
             const int L = xb + xi + k * R;
@@ -1399,14 +1420,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     const int tid = threadIdx.x, lane = tid & 63; // a library call on purpose: see wi_id_x
     // & 7: the compiler then knows each wave's DMA blocks stay inside one tile buffer
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & 7;
+    const int wr = KH ? (w & (NR - 1)) : w; // the wave's 32-row block of the item
+    const int kh = KH ? (w >> 2) : 0;       // and its half of each key tile
     const int l32 = lane & 31, hi = lane >> 5, g16 = lane >> 4, i16 = lane & 15;
-    // Key tiles of an item: all of them, or (causal) those up to its last row's limit,
-    // Sk - Sq + its last row (Sk >= Sq). Even for every item (host).
-    auto nkt_of = [&](int qt) {
-        if constexpr (CAUSAL)
-            return (Sk - Sq + min(Sq - 1, qt * BQ + BQ - 1)) / KT + 1;
-        return (Sk + KT - 1) / KT;
-    };
 
     const uint32_t qbytes = (uint32_t)Sq * (uint32_t)D * 2u; // one head of Q (O: twice; < 2^31)
     // Q rows of item (h, qt) for this lane's operand layout: 16-byte buffer loads, rows past Sq
@@ -1417,7 +1433,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         // r is made opaque here (and in store_o, and kbase in the last tile's mask): the
         // offsets and key compares are the same for every item, and hoisted out of the item
         // loop they would hold their registers (64 lane masks, 24 offsets) for the whole kernel.
-        int r = w * 32 + l32;
+        int r = wr * 32 + l32;
         asm volatile("" : "+v"(r));
         r += qt * BQ; // row of the head
         const int dlim = (r < Sq) ? D : 0;
@@ -1466,7 +1482,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         for (int k = 0; k < PW; ++k)
             dma16<0>(rv, &vbuf(buf)[(w * PW + k) * 512], vso[k]);
     };
-    constexpr int NOST = DP / 8; // vector memory instructions of one store_o
+    // Column blocks (32 wide) of O that one wave stores: all, or (KH) its half of them.
+    constexpr int NDB = KH ? DP / 64 : DP / 32;
+    constexpr int NOST = NDB * 4; // vector memory instructions of one store_o
 
     const int kperm = (l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
     const int kfo = (kperm >> 3) * 8 * DP + (kperm & 7) * 16 + ((hi ^ ((kperm >> 3) & 1)) * 8);
@@ -1481,34 +1499,34 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             o[db][i] = 0.f;
-    f32x16 s[KT / 32];
-    bf16x8 pk[KT / 16];
+    f32x16 s[KW / 32];
+    bf16x8 pk[KW / 16];
     bf16x8 va[2][DP / 32];
 
     // S^T = K_tile . Q^T (the next sub-tile's K fragments read between this one's MFMAs).
     auto qk = [&](int buf) __attribute__((always_inline)) {
-        const uint16_t *kb0 = &kbuf(buf)[kfo];
+        const uint16_t *kb0 = &kbuf(buf)[kfo + kh * (KW / 32) * KSUB];
         bf16x8 ka[2][DP / 16];
 #pragma unroll
         for (int kk = 0; kk < DP / 16; ++kk)
             ka[0][kk] = as_bf16x8(*reinterpret_cast<const u32x4 *>(kb0 + kk * KDK));
         __builtin_amdgcn_sched_group_barrier(0x100, DP / 16, 0);
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t) {
+        for (int t = 0; t < KW / 32; ++t) {
 #pragma unroll
             for (int i = 0; i < 16; ++i)
                 s[t][i] = 0.f;
 #pragma unroll
             for (int kk = 0; kk < DP / 16; ++kk) {
                 s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[t & 1][kk], qb[kk], s[t], 0, 0, 0);
-                if (t + 1 < KT / 32)
+                if (t + 1 < KW / 32)
                     ka[(t + 1) & 1][kk] = as_bf16x8(
                         *reinterpret_cast<const u32x4 *>(kb0 + (t + 1) * KSUB + kk * KDK));
             }
 #pragma unroll
             for (int kk = 0; kk < DP / 16; ++kk) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (t + 1 < KT / 32)
+                if (t + 1 < KW / 32)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
         }
@@ -1520,7 +1538,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // sub-tile between the two is compared key by key.
     auto lims = [&](int qt, int &lo, int &wmax) {
         if constexpr (CAUSAL) {
-            const int qmin = qt * BQ + w * 32;
+            const int qmin = qt * BQ + wr * 32;
             lo = __builtin_amdgcn_readfirstlane(min(Sk - 1, Sk - Sq + qmin));
             wmax = __builtin_amdgcn_readfirstlane(
                 qmin < Sq ? min(Sk - 1, Sk - Sq + min(Sq - 1, qmin + 31)) : -1);
@@ -1532,15 +1550,15 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     auto mask = [&](int kbase, int qt) __attribute__((always_inline)) {
         int lo, wmax;
         lims(qt, lo, wmax);
-        if (kbase + KT - 1 > lo) {
+        if (kbase + KW - 1 > lo) {
             int lim = Sk - 1;
             if constexpr (CAUSAL) {
-                int r = w * 32 + l32;
+                int r = wr * 32 + l32;
                 asm volatile("" : "+v"(r));
                 lim = min(Sk - 1, Sk - Sq + qt * BQ + r);
             }
 #pragma unroll
-            for (int t = 0; t < KT / 32; ++t) {
+            for (int t = 0; t < KW / 32; ++t) {
                 const int k0t = kbase + t * 32;
                 if (k0t + 31 <= lo)
                     continue;
@@ -1570,16 +1588,20 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // fresh: an item's first tile, where l and o are still zero (o is then written, not
     // accumulated, by that tile's P.V): m rises with no rescale to apply.
     auto row_max = [&](auto fresh) __attribute__((always_inline)) {
-        float mt[KT / 32];
+        float mt[KW / 32];
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t) {
+        for (int t = 0; t < KW / 32; ++t) {
             float m = max3f(s[t][0], s[t][1], s[t][2]);
 #pragma unroll
             for (int i = 3; i < 15; i += 2)
                 m = max3f(m, s[t][i], s[t][i + 1]);
             mt[t] = fmaxf(m, s[t][15]);
         }
-        const float mx = max_xor32(fmaxf(max3f(mt[0], mt[1], mt[2]), mt[3]));
+        float mx = mt[0];
+#pragma unroll
+        for (int j = 1; j < KW / 32; j += 2)
+            mx = (j + 1 < KW / 32) ? max3f(mx, mt[j], mt[j + 1]) : fmaxf(mx, mt[j]);
+        mx = max_xor32(mx);
         const bool raise = mx > m_run;
         if constexpr (decltype(fresh)::value) {
             m_run = raise ? mx : m_run;
@@ -1595,9 +1617,9 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     };
     auto exps = [&]() __attribute__((always_inline)) -> float {
         const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
-        float ps[KT / 16];
+        float ps[KW / 16];
 #pragma unroll
-        for (int t = 0; t < KT / 32; ++t)
+        for (int t = 0; t < KW / 32; ++t)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 float p[8];
@@ -1610,11 +1632,12 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
         float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < KT / 16; ++j)
+        for (int j = 0; j < KW / 16; ++j)
             psum += ps[j];
         return psum;
     };
     auto vfrag = [&](int buf, int cc, int db) -> bf16x8 {
+        cc += kh * (KW / 16); // the wave's key half of the tile (KH)
         const uint16_t *vb = &vbuf(buf)[vfo + cc * 16 * DP + db * 128];
         return join_tr(lds_read_tr(vb), lds_read_tr(vb + 4 * DP));
     };
@@ -1626,46 +1649,104 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // fresh (an item's first tile): the first 16-key chunk starts the accumulators from zero.
     auto pv = [&](int buf, auto fresh) {
 #pragma unroll
-        for (int cc = 0; cc < KT / 16; ++cc) {
+        for (int cc = 0; cc < KW / 16; ++cc) {
 #pragma unroll
             for (int db = 0; db < DP / 32; ++db) {
                 const f32x16 acc =
                     (decltype(fresh)::value && cc == 0) ? f32x16{} : o[db];
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[cc & 1][db], pk[cc], acc, 0, 0,
                                                                0);
-                if (cc + 1 < KT / 16)
+                if (cc + 1 < KW / 16)
                     va[(cc + 1) & 1][db] = vfrag(buf, cc + 1, db);
             }
 #pragma unroll
             for (int db = 0; db < DP / 32; ++db) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (cc + 1 < KT / 16)
+                if (cc + 1 < KW / 16)
                     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             }
         }
     };
     // O of item (h, qt) from (o, l): NOST buffer stores whatever the data (none lands when
-    // !valid: every offset is then outside the descriptor's range).
+    // !valid: every offset is then outside the descriptor's range). KH: o[0 .. NDB) holds
+    // (kh_combine) the wave's column blocks kh * NDB .. of the rows, the partner wave's the
+    // others.
     auto store_o = [&](int h, int qt, bool valid) __attribute__((always_inline)) {
         const float lt = l_run + __shfl_xor(l_run, 32);
         const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(O + (size_t)h * Sq * D, 2u * qbytes);
-        int r = w * 32 + l32;
+        int r = wr * 32 + l32;
         asm volatile("" : "+v"(r));
         r += qt * BQ; // row of the head
         // One column limit per lane (D, or 0 for a row to drop): a single compare per store
         // keeps the stores free of branches.
         const int dlim = (valid & (r < Sq)) ? D : 0;
 #pragma unroll
-        for (int db = 0; db < DP / 32; ++db)
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                const int d = db * 32 + i4 * 8 + 4 * hi;
+                const int d = (kh * NDB + db) * 32 + i4 * 8 + 4 * hi;
                 const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv,
                                  o[db][4 * i4 + 2] * inv, o[db][4 * i4 + 3] * inv};
                 const uint32_t off = (d < dlim) ? (uint32_t)(r * D + d) * 4u : 0x80000000u;
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0, 0);
             }
+    };
+    // KH hand-over at an item's end, once every wave is past the barrier after the item's last
+    // tile (buffer pair buf): kh_put leaves each wave's (m, l) in kh_ml and the NDB column
+    // blocks its partner (w ^ 4: same rows, other key half) stores in the partner's own DMA
+    // blocks of buf (PW KB of K, then PW KB of V; 16 fp32 per lane and block, in lane order);
+    // after a barrier kh_combine merges them with log-sum-exp weights against the larger m (a
+    // half with no admissible key has m = -inf: weight 0) into o[0 .. NDB). Each wave reads back
+    // only its own DMA blocks, which its own next DMA into buf rewrites after those reads have
+    // returned. Blocks are chosen by value (selects on kh), not by a register index that
+    // depends on kh, which would move o to scratch memory.
+    static_assert(!KH || PW * 512 * 2 == 16 * 64 * 4, "hand-over block = a wave's DMA blocks");
+    auto kh_area = [&](int buf, int wave, int j) __attribute__((always_inline)) -> float * {
+        return reinterpret_cast<float *>(&(j ? vbuf(buf) : kbuf(buf))[wave * PW * 512]);
+    };
+    auto kh_put = [&](int buf) __attribute__((always_inline)) {
+        if constexpr (!KH)
+            return;
+        kh_ml[w * 128 + lane] = m_run;
+        kh_ml[w * 128 + 64 + lane] = l_run;
+#pragma unroll
+        for (int j = 0; j < NDB; ++j) {
+            const f32x16 t = kh ? o[j] : o[(NDB + j) % (DP / 32)]; // the partner's block j
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 v = {t[4 * i4], t[4 * i4 + 1], t[4 * i4 + 2], t[4 * i4 + 3]};
+                *reinterpret_cast<f32x4 *>(kh_area(buf, w ^ 4, j) + (i4 * 64 + lane) * 4) = v;
+            }
+        }
+    };
+    auto kh_combine = [&](int buf) __attribute__((always_inline)) {
+        if constexpr (!KH)
+            return;
+        const int p = w ^ 4;
+        const float m2 = kh_ml[p * 128 + lane], l2 = kh_ml[p * 128 + 64 + lane];
+        // Key half 0's and half 1's values, in that order in both waves: both get the same l.
+        const float m0 = kh ? m2 : m_run, m1 = kh ? m_run : m2;
+        const float l0 = kh ? l2 : l_run, l1 = kh ? l_run : l2;
+        const float mn = fmaxf(m0, m1);
+        const float a0 = (m0 == kNegInf) ? 0.f : fast_exp2((m0 - mn) * c);
+        const float a1 = (m1 == kNegInf) ? 0.f : fast_exp2((m1 - mn) * c);
+        l_run = __builtin_fmaf(l0, a0, l1 * a1);
+#pragma unroll
+        for (int j = 0; j < NDB; ++j) {
+            const f32x16 t = kh ? o[(NDB + j) % (DP / 32)] : o[j]; // this wave's block j
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 v =
+                    *reinterpret_cast<const f32x4 *>(kh_area(buf, w, j) + (i4 * 64 + lane) * 4);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float x0 = kh ? v[jj] : t[4 * i4 + jj];
+                    const float x1 = kh ? t[4 * i4 + jj] : v[jj];
+                    o[j][4 * i4 + jj] = __builtin_fmaf(x0, a0, x1 * a1);
+                }
+            }
+        }
     };
 
     // Phase stamps (ATTN_PHASE_STAMPS builds): slot 0 at entry, 1 when the first item's Q and
@@ -1695,6 +1776,14 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         constexpr bool FIRST = decltype(kfirst)::value, LAST = decltype(klast)::value;
         constexpr int buf = decltype(kbuf)::value;
         const bool more = k + 1 < nmine;
+        if constexpr (KH && FIRST) {
+            // The previous item's key halves (left in buffer pair buf ^ 1 after its last tile),
+            // before the DMA below rewrites that pair.
+            if (k > 0) {
+                kh_combine(buf ^ 1);
+                __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0): the reads have returned
+            }
+        }
         // The next tile's DMA, the oldest vector memory operation of the tile.
         if (!LAST) {
             dma_kv(u, kt + 1, buf ^ 1);
@@ -1716,6 +1805,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         int kbase = kt * KT;
         if constexpr (LAST || CAUSAL)
             asm volatile("" : "+s"(kbase));
+        kbase += kh * KW; // the wave's first key of the tile
         int lo, wmax;
         lims(qt, lo, wmax);
         // Causal: a wave whose rows see no key of the last tile (the first half of the waves
@@ -1754,28 +1844,86 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             }
             l_run += psum;
         }
-        if (!(CAUSAL && LAST) || kbase <= wmax)
+        if (!(CAUSAL && LAST) || kbase <= wmax) {
             pv(buf, std::integral_constant<bool, FIRST>{});
+        } else if constexpr (FIRST) {
+            // (KH: an item of one key tile whose half has no key for this wave's rows.)
+#pragma unroll
+            for (int db = 0; db < DP / 32; ++db)
+                o[db] = f32x16{};
+        }
         if (!LAST || more) {
             // Wait for the next tile's DMA only: the O stores of tile 0 (NOST) are younger and
             // stay in flight. The last tile waits for everything (the next item's Q loads, issued
             // mid-tile, have landed by then), so each item starts with no vector memory operation
             // in flight: with one still pending at the item loop's head the compiler waits for it
             // before the first tile's LDS reads.
-            if (FIRST)
+            if (FIRST && !LAST)
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm(NOST));
             else
                 __builtin_amdgcn_s_waitcnt(0x0F70);
             __syncthreads();
         }
+        if constexpr (KH && LAST) {
+            if (!more)
+                __syncthreads(); // every wave is done with buffer pair buf
+            kh_put(buf);
+            __syncthreads();
+        }
     };
-    for (int k = 0; k < nmine; ++k) {
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    // KH: one unit per workgroup (host), its item of even key-tile count first (item): that
+    // one's tiles alternate from buffer 0 and end in buffer 1, so the other, of odd count,
+    // starts in buffer 0 and ends there too, and every step's buffers stay constants. The two
+    // items are written out rather than looped over: in a loop the compiler keeps values of
+    // every step instance live across it, and spills.
+    if constexpr (KH) {
+        {
+            int h, qt;
+            item(0, h, qt);
+            const int u = __builtin_amdgcn_readfirstlane(h / g);
+            const int nkt = __builtin_amdgcn_readfirstlane(nkt_of(qt));
+            phase_stamp(w, lane, 2);
+            step(u, qt, 0, 0, B0{}, std::true_type{}, std::false_type{});
+            phase_stamp(w, lane, 3);
+            for (int kt = 1; kt + 1 < nkt; kt += 2) {
+                step(u, qt, kt, 0, B1{}, std::false_type{}, std::false_type{});
+                step(u, qt, kt + 1, 0, B0{}, std::false_type{}, std::false_type{});
+            }
+            phase_stamp(w, lane, 4);
+            step(u, qt, nkt - 1, 0, B1{}, std::false_type{}, std::true_type{});
+            phase_stamp(w, lane, 5);
+        }
+        {
+            int h, qt;
+            item(1, h, qt);
+            const int u = __builtin_amdgcn_readfirstlane(h / g);
+            const int nkt = __builtin_amdgcn_readfirstlane(nkt_of(qt));
+            phase_stamp(w, lane, 6);
+            if (nkt == 1) {
+                step(u, qt, 0, 1, B0{}, std::true_type{}, std::true_type{});
+                phase_stamp(w, lane, 7);
+                phase_stamp(w, lane, 8);
+            } else {
+                step(u, qt, 0, 1, B0{}, std::true_type{}, std::false_type{});
+                phase_stamp(w, lane, 7);
+                for (int kt = 1; kt + 2 < nkt; kt += 2) {
+                    step(u, qt, kt, 1, B1{}, std::false_type{}, std::false_type{});
+                    step(u, qt, kt + 1, 1, B0{}, std::false_type{}, std::false_type{});
+                }
+                step(u, qt, nkt - 2, 1, B1{}, std::false_type{}, std::false_type{});
+                phase_stamp(w, lane, 8);
+                step(u, qt, nkt - 1, 1, B0{}, std::false_type{}, std::true_type{});
+            }
+            phase_stamp(w, lane, 9);
+        }
+    }
+    for (int k = 0; !KH && k < nmine; ++k) {
         int h, qt;
         item(k, h, qt);
         const int u = __builtin_amdgcn_readfirstlane(h / g);
         const int nkt = __builtin_amdgcn_readfirstlane(nkt_of(qt));
-        using B0 = std::integral_constant<int, 0>;
-        using B1 = std::integral_constant<int, 1>;
         phase_stamp(w, lane, 2 + 4 * k);
         step(u, qt, 0, k, B0{}, std::true_type{}, std::false_type{});
         phase_stamp(w, lane, 3 + 4 * k);
@@ -1790,6 +1938,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     {
         int hl, qtl;
         item(nmine - 1, hl, qtl);
+        if constexpr (KH)
+            kh_combine(0); // the last tile's buffer pair
         store_o(hl, qtl, true);
     }
 #if ATTN_PHASE_STAMPS
@@ -2912,22 +3062,35 @@ static bool prefill_persist_fits(int Hq, int Sq, int Sk, int D, bool causal) {
     return true;
 }
 
+// Whether a causal grid suits the persistent prefill with key halves: exactly two 128-row
+// query tiles per CU (where the per-tile kernel would run key halves in two rounds), so that
+// each workgroup runs one pair (the kernel's buffer order assumes at most one); whole tiles
+// (Sq % 128 == 0: a pair's key-tile counts then add up to an odd number), an even tile count
+// per head (the pairs) and Sk >= Sq (every row sees key 0).
+static bool prefill_persist_kh_fits(int Hq, int Sq, int Sk, int D) {
+    const int nqt = Sq / 128;
+    return Sk >= Sq && Sq % 128 == 0 && nqt % 2 == 0 && device_cus() % 8 == 0 &&
+           (long)Hq * nqt == 2L * device_cus() && (long)Sq * D * 4 < 0x7fffffffL;
+}
+
 // One workgroup per CU (a multiple of 8: each XCD takes the same count), each running its
-// items of the 256-row tiling back to back (causal: pairs of items).
-template <int DP, bool CAUSAL>
+// items of the 256-row tiling (KH: 128-row) back to back (causal: pairs of items).
+template <int DP, bool CAUSAL, bool KH = false>
 hipError_t launch_prefill_persist(const uint16_t *Q, const uint16_t *K, const uint16_t *V,
                                   float *O, int Hq, int Hkv, int Sq, int Sk, int D, float c,
                                   hipStream_t st) {
-    const int nqt = (Sq + 255) / 256;
+    constexpr int BQ = KH ? 128 : 256;
+    const int nqt = (Sq + BQ - 1) / BQ;
     const long nunits = (long)Hq * nqt / (CAUSAL ? 2 : 1);
     const int nwg = device_cus() / 8 * 8;
-    if (nunits <= 0 || nunits > 0x3fffffffL || nwg <= 0)
+    if (nunits <= 0 || nunits > 0x3fffffffL || nwg <= 0 || (KH && nunits > nwg))
         return hipErrorInvalidValue;
     if (t_plan)
-        plan_note(dim3((unsigned)nwg), dim3(512), "attn_prefill_persist_kernel<%d, %s> units=%ld",
-                  DP, tf(CAUSAL), nunits);
+        plan_note(dim3((unsigned)nwg), dim3(512),
+                  "attn_prefill_persist_kernel<%d, %s, %s> units=%ld", DP, tf(CAUSAL), tf(KH),
+                  nunits);
     else
-        hipLaunchKernelGGL((attn_prefill_persist_kernel<DP, CAUSAL>), dim3((unsigned)nwg),
+        hipLaunchKernelGGL((attn_prefill_persist_kernel<DP, CAUSAL, KH>), dim3((unsigned)nwg),
                            dim3(512), 0, st, Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, nqt, (int)nunits,
                            nwg);
     return hipGetLastError();
@@ -2953,10 +3116,17 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                                                   c, pm, pl, pacc, slots, st);
     }
     if constexpr (DP >= 64 && DP <= 128 && KT == 128)
-        if (nw == 4 && !hs && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(DP, Hq, Sq, Sk, CAUSAL))
+        if (nw == 4 && !hs && !prefill_pack(Hq, Hkv, Sq) && prefill_kh(DP, Hq, Sq, Sk, CAUSAL)) {
+            // Causal grids of two 128-row tiles per CU with row-major V run their key halves
+            // persistent: each CU's heavy and light tile in one workgroup.
+            if constexpr (DP == 128 && CAUSAL && !VT)
+                if (prefill_persist() && prefill_persist_kh_fits(Hq, Sq, Sk, D))
+                    return launch_prefill_persist<DP, CAUSAL, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
+                                                                    D, c, st);
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
                                                                        D, c, pm, pl, pacc, slots,
                                                                        st);
+        }
     // Grids of at least two rounds of 8-wave workgroups with row-major V whose items suit it
     // run persistent (attn_prefill_persist_kernel).
     if constexpr (DP == 128 && KT == 128 && !VT)

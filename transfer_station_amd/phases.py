@@ -26,12 +26,13 @@ from . import attn as ts
 from . import build as _build
 
 TICK_US = 0.01  # s_memrealtime runs at 100 MHz
-KT, BQ = 128, 256  # the persistent kernel's key tile and item rows
+KT, BQ = 128, 256  # the persistent kernel's key tile and item rows (128 with key halves)
 
 
-def items_of(b, nwg, nunits, g, nqt, causal):
+def items_of(b, nwg, nunits, g, nqt, causal, swap=None):
     """(query tile) of each item of workgroup b, in order: the kernel's item mapping
-    (attn_prefill_persist_kernel's `item`), restated."""
+    (attn_prefill_persist_kernel's `item`), restated. swap(qt) (key halves): whether a pair
+    whose heavy tile is qt runs its light tile first."""
     x, xi, R = b & 7, b >> 3, nwg >> 3
     per, rem = nunits >> 3, nunits & 7
     xb = x * (per + 1) if x < rem else rem * (per + 1) + (x - rem) * per
@@ -44,7 +45,10 @@ def items_of(b, nwg, nunits, g, nqt, causal):
             P = xb + xi + (k >> 1) * R
             rr = P - (P // (g * npair)) * (g * npair)
             pp = rr // g
-            out.append(pp if k & 1 else nqt - 1 - pp)
+            first, second = nqt - 1 - pp, pp
+            if swap is not None and swap(first):
+                first, second = second, first
+            out.append(second if k & 1 else first)
         else:
             L = xb + xi + k * R
             rr = L - (L // (g * nqt)) * (g * nqt)
@@ -52,27 +56,30 @@ def items_of(b, nwg, nunits, g, nqt, causal):
     return out
 
 
-def key_tiles(qt, Sq, Sk, causal):
+def key_tiles(qt, Sq, Sk, causal, bq=BQ):
     if causal:
-        return (Sk - Sq + min(Sq - 1, qt * BQ + BQ - 1)) // KT + 1
+        return (Sk - Sq + min(Sq - 1, qt * bq + bq - 1)) // KT + 1
     return (Sk + KT - 1) // KT
 
 
-def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal):
-    """Phase times in microseconds from the (workgroups, slots) stamp array."""
+def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal, kh=False):
+    """Phase times in microseconds from the (workgroups, slots) stamp array. kh: the key-halves
+    variant (128-row items, each pair's item of even key-tile count first)."""
     nwg = stamps.shape[0]
-    g, nqt = Hq // Hkv, (Sq + BQ - 1) // BQ
+    bq = 128 if kh else BQ
+    g, nqt = Hq // Hkv, (Sq + bq - 1) // bq
     nunits = Hq * nqt // (2 if causal else 1)
-    busy = [b for b in range(nwg) if items_of(b, nwg, nunits, g, nqt, causal)]
+    swap = (lambda qt: key_tiles(qt, Sq, Sk, causal, bq) % 2 == 1) if kh else None
+    busy = [b for b in range(nwg) if items_of(b, nwg, nunits, g, nqt, causal, swap)]
     # workgroups without items return before their first stamp
     t = (stamps.astype(np.int64) - int(stamps[busy, 0].min())) * TICK_US
     prologue, first_x, last_x, tile, tail, gaps, ends = [], [], [], [], [], [], []
     for b in busy:
-        qts = items_of(b, nwg, nunits, g, nqt, causal)
+        qts = items_of(b, nwg, nunits, g, nqt, causal, swap)
         per_tile = []
         for k, qt in enumerate(qts):
             s = t[b, 2 + 4 * k: 6 + 4 * k]
-            n = key_tiles(qt, Sq, Sk, causal)
+            n = key_tiles(qt, Sq, Sk, causal, bq)
             if n > 2:
                 per_tile.append((s[2] - s[1]) / (n - 2))
             if k + 1 < len(qts):
@@ -80,10 +87,11 @@ def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal):
         mid = float(np.median(per_tile)) if per_tile else float("nan")
         tile.extend(per_tile)
         prologue.append(t[b, 1] - t[b, 0])
-        for k in range(len(qts)):
+        for k, qt in enumerate(qts):
             s = t[b, 2 + 4 * k: 6 + 4 * k]
             first_x.append(s[1] - s[0] - mid)
-            last_x.append(s[3] - s[2] - mid)
+            if key_tiles(qt, Sq, Sk, causal, bq) > 1:  # (an item of one tile: first only)
+                last_x.append(s[3] - s[2] - mid)
         tail.append(t[b, slots - 1] - t[b, 2 + 4 * (len(qts) - 1) + 3])
         ends.append(t[b, slots - 1])
 
@@ -216,7 +224,8 @@ def timeline(Hq, Hkv, Sq, Sk, D, causal=0, seed=0x12345678, warm_s=0.3):
         run(L.attn_flash, 10)  # back to back: the stamps hold the last call's, warm
         stamps = st.download(np.uint64, nwg * slots).reshape(nwg, slots)
         if kernel.startswith("attn_prefill_persist_kernel"):
-            summary = summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal)
+            kh = kernel.replace(" ", "").endswith(",true>")  # <DP, CAUSAL, KH>
+            summary = summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal, kh)
         else:
             summary = summarize_tiles(stamps, slots)
         summary.update({"shape": [Hq, Hkv, Sq, Sk, D, causal], "kernel": kernel,
