@@ -644,6 +644,10 @@ PLANS = [
     ("c3 4k", 128, 32, 4096, 4096, 128, 0, 0, [("attn_prefill_persist_kernel<128, false, false>", "units=2048")]),
     ("c3 4k causal", 128, 32, 4096, 4096, 128, 1, 0,
      [("attn_prefill_persist_kernel<128, true, false>", "units=1024")]),
+    ("c3 1k causal", 128, 32, 1024, 1024, 128, 1, 0,
+     [("attn_prefill_persist_kernel<128, true, false>", "units=256")]),
+    ("96 heads at 1536 causal (288 pairs: uneven)", 96, 24, 1536, 1536, 128, 1, 0,
+     [("attn_prefill_fast_kernel<128, 64, 4, true, false, false>", "nsplit=1")]),
     ("c3 4k, V^T", 128, 32, 4096, 4096, 128, 0, 1,
      [("attn_prefill_fast_kernel<128, 128, 8, false, true, false>", "nsplit=1")]),
     ("c4 MQA 2k", 128, 8, 2048, 2048, 128, 0, 0, [("attn_prefill_persist_kernel<128, false, false>", "units=1024")]),

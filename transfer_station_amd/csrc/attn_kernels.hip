@@ -2957,14 +2957,18 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
 //    Qwen3 causal 1k / 2k / 4k +18% / +9% / +7.5%, config 5 causal +24%. When 256-row tiles
 //    are part empty (Sq = 128, 200), 4 waves add no parallelism and their 64-key tiles lose
 //    11-20%; above the small-grid sizes 8 waves win by 5-9%.
-// ATTN_PREFILL_WAVES=4 or =8 forces one for tuning sweeps.
-static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head_split) {
+// ATTN_PREFILL_WAVES=4 or =8 (read once) forces one for tuning sweeps.
+static int prefill_waves_forced() {
     static int forced = -1;
     if (forced < 0) {
         const char *e = getenv("ATTN_PREFILL_WAVES");
         forced = (e && (atoi(e) == 4 || atoi(e) == 8)) ? atoi(e) : 0;
     }
-    if (forced)
+    return forced;
+}
+
+static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head_split) {
+    if (const int forced = prefill_waves_forced())
         return forced;
     const int g = Hq / Hkv;
     if (prefill_pack(Hq, Hkv, Sq)) {
@@ -2977,7 +2981,9 @@ static int prefill_waves(int Hq, int Hkv, int Sq, int Sk, bool causal, bool head
     const bool full = (long)Sq * 10 >= t8 * 256 * 9;
     // Causal query tiles attend Sk - Sq/2 keys on average; up to 1024 their fixed cost per
     // workgroup (prologue, O stores, dispatch) is large enough that two resident 4-wave
-    // workgroups per CU, which overlap it, win: c3-shaped 1k / 2k causal +15% / +3%, 4k -1%.
+    // workgroups per CU, which overlap it, win against 8-wave per-tile workgroups: c3-shaped
+    // 1k / 2k causal +15% / +3%, 4k -1%. (Where the persistent kernel's pairs fit, that kernel
+    // runs instead: launch_prefill_fast_t.)
     const bool short_causal = causal && (long)Sk - Sq / 2 <= 1024;
     // head_split: the 4-wave grid takes the slot-balanced head split (prefill_head_split).
     return (head_split ||
@@ -3128,11 +3134,22 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
                                                                        st);
         }
     // Grids of at least two rounds of 8-wave workgroups with row-major V whose items suit it
-    // run persistent (attn_prefill_persist_kernel).
-    if constexpr (DP == 128 && KT == 128 && !VT)
-        if (nw == 8 && prefill_persist() && !prefill_pack(Hq, Hkv, Sq) &&
+    // run persistent (attn_prefill_persist_kernel). So do causal grids that take 4-wave
+    // workgroups for their short key ranges (prefill_waves) when their pairs of 256-row items
+    // fill the CUs evenly (at most 10% of the pair slots idle): same box, 4-wave -> persistent,
+    // c3 shape at 1k causal 47.4 -> 46.0 us, 1000 rows 47.1 -> 45.6, 2k 144.8 -> 140.0, 64 heads
+    // at 2k 75.9 -> 72.7, MQA-like 128 heads over 8 kv heads at 1k 45.0 -> 45.9; unevenly
+    // (96 heads at 1536: 288 pairs on 256 CUs) 67.6 -> 98.9.
+    if constexpr (DP == 128 && KT == 128 && !VT) {
+        bool persist = nw == 8;
+        if (CAUSAL && nw == 4 && !prefill_waves_forced()) {
+            const long units = (long)Hq * ((Sq + 255) / 256) / 2, nwg = device_cus() / 8 * 8;
+            persist = nwg > 0 && 10 * (((units + nwg - 1) / nwg) * nwg - units) <= units;
+        }
+        if (persist && prefill_persist() && !prefill_pack(Hq, Hkv, Sq) &&
             prefill_persist_fits(Hq, Sq, Sk, D, CAUSAL))
             return launch_prefill_persist<DP, CAUSAL>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c, st);
+    }
     if constexpr (DP <= 128 && KT * DP / 8 >= 512) // every thread of 8 waves stages a chunk
         if (nw == 8)
             return launch_prefill_fast_nw<DP, KT, 8, CAUSAL, VT>(Q, K, V, O, Hq, Hkv, Sq, Sk, D, c,
