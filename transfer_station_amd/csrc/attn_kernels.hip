@@ -1333,7 +1333,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 //     descriptor's range: the count never depends on the data), issued in the next item's first
 //     tile after that tile's DMA; the wait for the DMA then leaves exactly those 16 stores in
 //     flight (vmcnt(16): vector memory operations complete in issue order), so the O write
-//     burst drains under the next tile's compute.
+//     burst drains under the next tile's compute. The stores are non-temporal and each writes
+//     whole 128-byte lines (store_o), so O does not evict the K/V tiles from L2.
 // Items of a CU follow the non-persistent grid's rounds: XCD x = b % 8 holds the logical items
 // [xb, xb + nx) (kv-head-major, as xcd_remap deals them) and its i-th workgroup takes
 // xb + i, xb + i + R, ... (R workgroups per XCD), so each round of an XCD shares one kv head's
@@ -1671,26 +1672,66 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // !valid: every offset is then outside the descriptor's range). KH: o[0 .. NDB) holds
     // (kh_combine) the wave's column blocks kh * NDB .. of the rows, the partner wave's the
     // others.
+    // Each store writes whole 128-byte lines, non-temporally: a lane holds 16-byte chunks
+    // hi, 2 + hi, 4 + hi, 6 + hi (i4 = 0..3) of its row's 32-column block, so two lane/register
+    // bit swaps (row bit 4 with i4 bit 1 by v_permlane16_swap, row bit 3 with i4 bit 0 by a
+    // DPP exchange with lane ^ 8) leave each register holding, per lane, chunk
+    // c8 = hi + 2 (lane bit 3) + 4 (lane bit 4) of row (lane & 7) + 8 s0 + 16 s1: one store then
+    // covers 8 rows x 128 bytes. Partial-line stores left through L2 (whole-line ones with the
+    // ordinary policy measured within 1%), where they evicted the K/V tiles of the next items;
+    // non-temporal partial lines were written back piecemeal (2.35x the bytes).
     auto store_o = [&](int h, int qt, bool valid) __attribute__((always_inline)) {
         const float lt = l_run + __shfl_xor(l_run, 32);
         const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(O + (size_t)h * Sq * D, 2u * qbytes);
-        int r = wr * 32 + l32;
+        int r = wr * 32 + (lane & 7);
         asm volatile("" : "+v"(r));
-        r += qt * BQ; // row of the head
-        // One column limit per lane (D, or 0 for a row to drop): a single compare per store
-        // keeps the stores free of branches.
-        const int dlim = (valid & (r < Sq)) ? D : 0;
+        r += qt * BQ; // row of the head for s0 = s1 = 0
+        const int c8 = hi + 2 * ((lane >> 3) & 1) + 4 * ((lane >> 4) & 1);
+        const bool b3 = (lane >> 3) & 1;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+        for (int db = 0; db < NDB; ++db) {
+            float x[4][4]; // [s1 s0][j] after the swaps; [i4][j] before
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const int d = (kh * NDB + db) * 32 + i4 * 8 + 4 * hi;
-                const f32x4 v = {o[db][4 * i4] * inv, o[db][4 * i4 + 1] * inv,
-                                 o[db][4 * i4 + 2] * inv, o[db][4 * i4 + 3] * inv};
-                const uint32_t off = (d < dlim) ? (uint32_t)(r * D + d) * 4u : 0x80000000u;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                float v[4];
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    v[i4] = o[db][4 * i4 + j] * inv;
+#pragma unroll
+                for (int a = 0; a < 2; ++a) { // row bit 4 <-> i4 bit 1
+                    const auto sw = __builtin_amdgcn_permlane16_swap(
+                        __builtin_bit_cast(unsigned, v[a]), __builtin_bit_cast(unsigned, v[a + 2]),
+                        false, false);
+                    v[a] = __builtin_bit_cast(float, (unsigned)sw[0]);
+                    v[a + 2] = __builtin_bit_cast(float, (unsigned)sw[1]);
+                }
+#pragma unroll
+                for (int s1 = 0; s1 < 2; ++s1) { // row bit 3 <-> i4 bit 0
+                    const float X = v[2 * s1], Y = v[2 * s1 + 1];
+                    const float Xo = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, X), 0x128,
+                                                           0xf, 0xf, false)); // row_ror:8 = lane ^ 8
+                    const float Yo = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, Y), 0x128,
+                                                           0xf, 0xf, false));
+                    x[2 * s1][j] = b3 ? Yo : X;
+                    x[2 * s1 + 1][j] = b3 ? Y : Xo;
+                }
             }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { // q = 2 s1 + s0: rows + 8 s0 + 16 s1
+                const int rq = r + 8 * (q & 1) + 16 * (q >> 1);
+                // One column limit per lane (D, or 0 for a row to drop): a single compare per
+                // store keeps the stores free of branches.
+                const int dlim = (valid & (rq < Sq)) ? D : 0;
+                const int d = (kh * NDB + db) * 32 + 4 * c8;
+                const f32x4 v = {x[q][0], x[q][1], x[q][2], x[q][3]};
+                const uint32_t off = (d < dlim) ? (uint32_t)(rq * D + d) * 4u : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0,
+                                                       2 /* nt */);
+            }
+        }
     };
     // KH hand-over at an item's end, once every wave is past the barrier after the item's last
     // tile (buffer pair buf): kh_put leaves each wave's (m, l) in kh_ml and the NDB column
@@ -1766,11 +1807,12 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // O leaves, then the row max), LAST (kt = nkt - 1: the next item's tile 0 DMA and Q loads,
     // the mask, the row max) or neither (the sum test, a rare recompute). Item coordinates are
     // recomputed from the item index where needed rather than carried in registers.
-    // Every item's nkt is even (host), so tile kt uses LDS buffer kt & 1: each step's buffers
-    // are constants, which lets the compiler tell this tile's LDS reads from the next tile's DMA
-    // (with a run-time buffer index it waits for that DMA before the first read).
-    // Causal: FIRST and middle tiles are masked too where they reach past the wave's first
-    // row's limit.
+    // Every item's nkt is even (host), so tile kt uses LDS buffer kt & 1 (KH: the item order
+    // below fixes the buffers of odd counts): each step's buffers are constants, which lets the
+    // compiler tell this tile's LDS reads from the next tile's DMA (with a run-time buffer index
+    // it waits for that DMA before the first read). FIRST and LAST are one step for a KH item of
+    // one key tile. Causal: FIRST and middle tiles are masked too where they reach past the
+    // wave's first row's limit.
     auto step = [&](int u, int qt, int kt, int k, auto kbuf, auto kfirst, auto klast)
         __attribute__((always_inline)) {
         constexpr bool FIRST = decltype(kfirst)::value, LAST = decltype(klast)::value;
