@@ -1674,8 +1674,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // others.
     // Each store writes whole 128-byte lines, non-temporally: a lane holds 16-byte chunks
     // hi, 2 + hi, 4 + hi, 6 + hi (i4 = 0..3) of its row's 32-column block, so two lane/register
-    // bit swaps (row bit 4 with i4 bit 1 by v_permlane16_swap, row bit 3 with i4 bit 0 by a
-    // DPP exchange with lane ^ 8) leave each register holding, per lane, chunk
+    // bit swaps (row bit 4 with i4 bit 1 by v_permlane16_swap, row bit 3 with i4 bit 0 by two
+    // bank-masked DPP moves from lane ^ 8) leave each register holding, per lane, chunk
     // c8 = hi + 2 (lane bit 3) + 4 (lane bit 4) of row (lane & 7) + 8 s0 + 16 s1: one store then
     // covers 8 rows x 128 bytes. Partial-line stores left through L2 (whole-line ones with the
     // ordinary policy measured within 1%), where they evicted the K/V tiles of the next items;
@@ -1688,7 +1688,6 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         asm volatile("" : "+v"(r));
         r += qt * BQ; // row of the head for s0 = s1 = 0
         const int c8 = hi + 2 * ((lane >> 3) & 1) + 4 * ((lane >> 4) & 1);
-        const bool b3 = (lane >> 3) & 1;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             float x[4][4]; // [s1 s0][j] after the swaps; [i4][j] before
@@ -1708,15 +1707,14 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
                 }
 #pragma unroll
                 for (int s1 = 0; s1 < 2; ++s1) { // row bit 3 <-> i4 bit 0
-                    const float X = v[2 * s1], Y = v[2 * s1 + 1];
-                    const float Xo = __builtin_bit_cast(
-                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, X), 0x128,
-                                                           0xf, 0xf, false)); // row_ror:8 = lane ^ 8
-                    const float Yo = __builtin_bit_cast(
-                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, Y), 0x128,
-                                                           0xf, 0xf, false));
-                    x[2 * s1][j] = b3 ? Yo : X;
-                    x[2 * s1 + 1][j] = b3 ? Y : Xo;
+                    // row_ror:8 reads lane ^ 8; the bank mask writes only the lanes with bit 3
+                    // set (banks 2, 3 of each row: 0xc) or clear (0x3), the others keep old.
+                    const int X = __builtin_bit_cast(int, v[2 * s1]);
+                    const int Y = __builtin_bit_cast(int, v[2 * s1 + 1]);
+                    x[2 * s1][j] =
+                        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(X, Y, 0x128, 0xf, 0xc, false));
+                    x[2 * s1 + 1][j] =
+                        __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(Y, X, 0x128, 0xf, 0x3, false));
                 }
             }
 #pragma unroll
