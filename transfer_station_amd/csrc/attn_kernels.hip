@@ -1329,10 +1329,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 //   * the next item's Q (registers) is loaded during the last tile, after its S^T, so it lands
 //     under the softmax and P.V (the last tile takes the row max, so no recompute needs the
 //     old Q);
-//   * an item's O leaves as 16 buffer stores per lane (rows past Sq fall outside the
-//     descriptor's range: the count never depends on the data), issued in the next item's first
-//     tile after that tile's DMA; the wait for the DMA then leaves exactly those 16 stores in
-//     flight (vmcnt(16): vector memory operations complete in issue order), so the O write
+//   * an item's O leaves as NOST = 16 buffer stores per lane (8 with KH; rows past Sq fall
+//     outside the descriptor's range: the count never depends on the data), issued in the next
+//     item's first tile after that tile's DMA; the wait for the DMA then leaves exactly those
+//     stores in flight (vmcnt(NOST): vector memory operations complete in issue order), so the O write
 //     burst drains under the next tile's compute. The stores are non-temporal and each writes
 //     whole 128-byte lines (store_o), so O does not evict the K/V tiles from L2.
 // Items of a CU follow the non-persistent grid's rounds: XCD x = b % 8 holds the logical items
