@@ -1832,16 +1832,19 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
             item(k + 1, hn, qtn);
             dma_kv(__builtin_amdgcn_readfirstlane(hn / g), 0, buf ^ 1);
         }
-        if (FIRST) {
-            // The previous item's O (after this tile's DMA; for the first item the stores are
-            // issued but land nowhere, which keeps this tile free of branches), then a fresh
-            // state.
+        // The previous item's O (after this tile's DMA; for the first item the stores are
+        // issued but land nowhere, which keeps this tile free of branches), then a fresh state.
+        // KH issues them after this tile's S^T instead (its registers leave room to keep its O
+        // half live across it): 0-2% faster, bit-identical.
+        auto leave_o = [&]() __attribute__((always_inline)) {
             int hp, qtp;
             item(k > 0 ? k - 1 : 0, hp, qtp);
             store_o(hp, qtp, k > 0);
             m_run = kNegInf;
             l_run = 0.f; // o: written by this tile's P.V
-        }
+        };
+        if constexpr (FIRST && !KH)
+            leave_o();
         int kbase = kt * KT;
         if constexpr (LAST || CAUSAL)
             asm volatile("" : "+s"(kbase));
@@ -1853,6 +1856,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
         // but still computes S^T: skipping that too made the compiler spill about 100
         // registers.
         qk(buf);
+        if constexpr (FIRST && KH)
+            leave_o();
         pv_first(buf);
         // The fast kernel's phase order: S^T, then the softmax, then P.V (letting the compiler
         // move the first sub-tile's exponentials between the later sub-tiles' MFMAs measured
