@@ -52,6 +52,9 @@ def test_summary_of_synthetic_stamps():
     assert s["first_tile_extra_us"]["median"] == 1.0 and s["last_tile_extra_us"]["median"] == 2.0
     assert s["between_items_us"]["max"] == 0.0 and s["tail_us"]["median"] == 5.0
     assert abs(s["span_us"] - (1.5 + 4 + 2 * 27 + 5)) < 1e-9
+    assert [it["item"] for it in s["items"]] == [0, 1]
+    assert all(it["key_tiles"] == 8 and it["first_tile_extra_us"]["median"] == 1.0 and
+               it["last_tile_extra_us"]["median"] == 2.0 for it in s["items"])
 
 
 def test_key_halves_pairs_run_the_even_count_first():

@@ -1,7 +1,7 @@
 """Phase timeline of the persistent prefill (attn_prefill_persist_kernel), from stamps written
 inside the kernel.
 
-    python -m transfer_station_amd.phases [--shape Hq,Hkv,Sq,Sk,D[,causal]] [--json]
+    python -m transfer_station_amd.phases [--shape Hq,Hkv,Sq,Sk,D[,causal]] [--json] [--items]
 
 The stamps exist only in libattn_flash_stamps.so, the library built a second time with
 ATTN_PHASE_STAMPS=1 (transfer_station_amd/build.py); the product library has none of that code.
@@ -74,6 +74,7 @@ def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal, kh=False):
     # workgroups without items return before their first stamp
     t = (stamps.astype(np.int64) - int(stamps[busy, 0].min())) * TICK_US
     prologue, first_x, last_x, tile, tail, gaps, ends = [], [], [], [], [], [], []
+    by_k = {}  # item index -> (key tiles, first-tile extra, last-tile extra) per workgroup
     for b in busy:
         qts = items_of(b, nwg, nunits, g, nqt, causal, swap)
         per_tile = []
@@ -89,9 +90,14 @@ def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal, kh=False):
         prologue.append(t[b, 1] - t[b, 0])
         for k, qt in enumerate(qts):
             s = t[b, 2 + 4 * k: 6 + 4 * k]
+            n = key_tiles(qt, Sq, Sk, causal, bq)
             first_x.append(s[1] - s[0] - mid)
-            if key_tiles(qt, Sq, Sk, causal, bq) > 1:  # (an item of one tile: first only)
+            d = by_k.setdefault(k, ([], [], []))
+            d[0].append(n)
+            d[1].append(s[1] - s[0] - mid)
+            if n > 1:  # (an item of one tile: first only)
                 last_x.append(s[3] - s[2] - mid)
+                d[2].append(s[3] - s[2] - mid)
         tail.append(t[b, slots - 1] - t[b, 2 + 4 * (len(qts) - 1) + 3])
         ends.append(t[b, slots - 1])
 
@@ -113,6 +119,10 @@ def summarize(stamps, slots, Hq, Hkv, Sq, Sk, causal, kh=False):
         "between_items_us": stat(gaps),
         "tail_us": stat(tail),
         "span_us": round(float(max(ends)), 3),
+        # per item index of a workgroup: the median key-tile count and first / last tile extras
+        "items": [{"item": k, "key_tiles": float(np.median(d[0])),
+                   "first_tile_extra_us": stat(d[1]), "last_tile_extra_us": stat(d[2])}
+                  for k, d in sorted(by_k.items())],
     }
 
 
@@ -260,6 +270,8 @@ def main():
                     help="Hq,Hkv,Sq,Sk,D[,causal] (repeatable; default: config 3 at 1k, 4k and "
                          "4k causal, the Qwen3 4k causal case and config 5)")
     ap.add_argument("--json", action="store_true", help="one JSON line per shape")
+    ap.add_argument("--items", action="store_true",
+                    help="persistent kernel: also the first / last tile extras by item index")
     args = ap.parse_args()
     shapes = [tuple(int(v) for v in s.split(",")) for s in args.shape] if args.shape else [
         (128, 32, 1024, 1024, 128, 0), (128, 32, 4096, 4096, 128, 0),
@@ -284,6 +296,11 @@ def main():
                                                               v["max"]))
             else:
                 print("  %-31s %9.2f" % (label, v))
+        for it in (summary.get("items") or []) if args.items else []:
+            f, l = it["first_tile_extra_us"], it["last_tile_extra_us"]
+            print("  item %d (%3.0f key tiles): first tile extra %5.2f, last tile extra %s" % (
+                it["item"], it["key_tiles"], f["median"] if f else float("nan"),
+                "%5.2f" % l["median"] if l else "  -"))
         print(flush=True)
 
 
