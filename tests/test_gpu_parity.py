@@ -380,23 +380,70 @@ def test_prefill_key_halves(oracle, Hq, Hkv, Sq, Sk, D, causal, ref_cap):
     assert np.array_equal(O.view(np.uint32), again.view(np.uint32))
 
 
-@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,sigma_q,ref_cap", [
-    (48, 12, 1000, 4000, 64, 4.0, 8),  # config 5: 384 tiles, the last 16 heads in key halves
-    (40, 10, 1000, 4000, 64, 1.0, 8),  # 320 tiles, 24 heads halved, 128 whole tiles
+HEAD_SPLIT_CASES = [
+    (48, 12, 1000, 4000, 64, 4.0, 8),  # config 5: 384 tiles (the last 16 heads halved); 252 x 192
+    (40, 10, 1000, 4000, 64, 1.0, 8),  # 320 tiles (24 heads halved); 210 x 192 rows
     (20, 5, 1800, 2056, 40, 1.0, 0),   # D = 40 on the 64-wide tiles, a key tail, every row
-])
+    (40, 40, 1000, 4000, 64, 1.0, 8),  # MHA: 6 workgroups per head, the last of 40 rows
+]
+
+
+@pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,sigma_q,ref_cap", HEAD_SPLIT_CASES)
 def test_prefill_head_split(oracle, Hq, Hkv, Sq, Sk, D, sigma_q, ref_cap):
-    """Non-causal D <= 64 grids of one to two 128-row tiles per CU run the last heads' tiles as
-    two key halves merged through the scratch, whole tiles in the CUs' first slots. The rows
-    the reference's row set picks are checked against the oracle (split and whole heads alike);
-    the V^T input takes the same split and gives the same bits, and a second call repeats
-    them."""
+    """Non-causal D <= 64 grids of one to two 128-row tiles per CU (where the 4-wave grid would
+    run the last heads' tiles as key halves merged through the scratch) run as 12-wave key-halves
+    workgroups of 192 rows of a kv head's packed row space (32-row blocks straddle query heads;
+    each kv head's last workgroup is part empty), one per CU. The rows the reference's row set
+    picks are checked against the oracle; the V^T input takes the same kernel and gives the same
+    bits, and a second call repeats them."""
+    if ts.device_info()["cus"] == 256:
+        plan = ts.attn_flash_plan(Hq, Hkv, Sq, Sk, D, 0)
+        assert [p[0] for p in plan] == ["attn_prefill_fast_kernel<64, 128, 12, false, false, true>"]
     Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, SEED0 + 90 + Hq, sigma_q=sigma_q)
-    O = check(oracle, "prefill head split", Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128, ref_cap=ref_cap)
+    O = check(oracle, "prefill 12 waves", Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128, ref_cap=ref_cap)
     Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, prepack_v=True)
     assert np.array_equal(O.view(np.uint32), Ot.view(np.uint32))
     again = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128)
     assert np.array_equal(O.view(np.uint32), again.view(np.uint32))
+
+
+_HSPLIT_SCRIPT = r"""
+import sys, numpy as np
+sys.path.insert(0, %r)
+import transfer_station_amd as ts
+from oracle import oracle as o
+for (Hq, Hkv, Sq, Sk, D, sigma_q, cap) in %r:
+    plan = ts.attn_flash_plan(Hq, Hkv, Sq, Sk, D, 0)
+    print("head split case", Hq, Hkv, Sq, Sk, D, plan, flush=True)
+    if ts.device_info()["cus"] == 256:
+        assert [p[0] for p in plan] == ["attn_prefill_fast_kernel<64, 128, 4, false, false, false>",
+                                        "attn_merge2_kernel"], plan
+        assert "hsplit=0" not in plan[0][1].split(), plan
+    Q, K, V = ts.synth_normal_qkv(Hq, Hkv, Sq, Sk, D, 90 + Hq, sigma_q=sigma_q)
+    O = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, 128)
+    rows = o.ref_rowset(Sq, cap)
+    R = o.attn_ref(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, rows, nthreads=8)
+    ok, mad, maxref, nbad = o.cmp_rows(R, O, Hq, Sq, D, rows)
+    print("   err/scale", mad / maxref, nbad, flush=True)
+    assert ok
+    Ot = ts.run_attention(Q, K, V, Hq, Hkv, Sq, Sk, D, 0, prepack_v=True)
+    assert np.array_equal(O.view(np.uint32), Ot.view(np.uint32))
+print("OK")
+"""
+
+
+def test_prefill_head_split_4_waves():
+    """The same grids with the 12-wave workgroups turned off (ATTN_PREFILL_W12=0, in a child
+    process) take 4-wave workgroups with the slot-balanced head split: whole tiles in the CUs'
+    first slots, the last heads' tiles as two key halves merged through the scratch
+    (attn_merge2_kernel)."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, ATTN_PREFILL_W12="0")
+    r = subprocess.run([sys.executable, "-c", _HSPLIT_SCRIPT % (root, HEAD_SPLIT_CASES[:3])],
+                       env=env, capture_output=True, text=True, timeout=240)
+    say(r.stdout[-2000:] + r.stderr[-2000:])
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK")
 
 
 @pytest.mark.parametrize("Hq,Hkv,Sq,Sk,D,causal", [
@@ -407,6 +454,7 @@ def test_prefill_head_split(oracle, Hq, Hkv, Sq, Sk, D, sigma_q, ref_cap):
     (128, 32, 1024, 1504, 128, 0),  # the persistent prefill (12 key tiles per item)
     (128, 32, 1024, 1024, 128, 1),  # the causal persistent prefill (pairs of 2 + 8, 4 + 6 tiles)
     (64, 16, 1024, 1024, 128, 1),  # the persistent prefill with key halves (pairs of 8 + 1 ...)
+    (24, 6, 1500, 2104, 64, 0),    # 12 waves on key halves, 192 packed rows, pipelined halves
 ])
 def test_score_jumps_between_key_tiles(oracle, Hq, Hkv, Sq, Sk, D, causal):
     """Each query row gets a first coordinate of +4 or -4 and each key a first coordinate that
@@ -652,6 +700,11 @@ PLANS = [
      [("attn_prefill_fast_kernel<128, 128, 8, false, true, false>", "nsplit=1")]),
     ("c4 MQA 2k", 128, 8, 2048, 2048, 128, 0, 0, [("attn_prefill_persist_kernel<128, false, false>", "units=1024")]),
     ("c5 ragged D 64", 48, 12, 1000, 4000, 64, 0, 0,
+     [("attn_prefill_fast_kernel<64, 128, 12, false, false, true>", "pack=1")]),
+    ("c5 ragged D 64, V^T", 48, 12, 1000, 4000, 64, 0, 1,
+     [("attn_prefill_fast_kernel<64, 128, 12, false, true, true>", "pack=1")]),
+    ("48 MHA heads of 1000 rows at D 64 (288 workgroups of 192 rows: head split)",
+     48, 48, 1000, 4000, 64, 0, 0,
      [("attn_prefill_fast_kernel<64, 128, 4, false, false, false>", "hsplit=16"),
       ("attn_merge2_kernel", "")]),
     ("Qwen3 4k causal", 16, 8, 4096, 4096, 128, 1, 0,

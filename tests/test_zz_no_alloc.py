@@ -51,7 +51,8 @@ def run_both(Hq, Hkv, Sq, Sk, D, causal, seed, v_prepacked=0):
 # (label, Hq, Hkv, Sq, Sk, D, causal, v_prepacked): pairs of a larger then a smaller call, each
 # on a path that writes partial slots and merges them: split-K decode (row-major V and V^T),
 # the causal prefill's split of its upper query tiles, the prefill key split of small grids, and
-# the slot-balanced head split (D <= 64).
+# the slot-balanced head split (D <= 64; MHA grids whose 192-row workgroups would not fit one
+# per CU).
 PAIRS = [
     (("decode split 32k", 32, 8, 1, 32768, 128, 0, 0),
      ("decode split 4k", 32, 8, 1, 4096, 128, 0, 0)),
@@ -59,8 +60,8 @@ PAIRS = [
      ("prefill causal split 2k MQA", 4, 1, 2048, 2048, 128, 1, 0)),
     (("prefill key split 8k causal", 32, 8, 512, 8192, 128, 1, 0),
      ("prefill key split 4k", 16, 4, 512, 4096, 128, 0, 0)),
-    (("prefill head split D64", 48, 12, 1000, 4000, 64, 0, 0),
-     ("prefill head split D40", 20, 5, 1800, 2056, 40, 0, 0)),
+    (("prefill head split D64", 48, 48, 1000, 4000, 64, 0, 0),
+     ("prefill head split D40", 46, 46, 1000, 2056, 40, 0, 0)),
     (("decode split 8k D64 V^T", 16, 4, 4, 8192, 64, 1, 1),
      ("decode split 1k D40", 8, 2, 2, 1000, 40, 0, 0)),
 ]

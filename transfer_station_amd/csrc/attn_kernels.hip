@@ -505,16 +505,19 @@ __device__ __forceinline__ unsigned long long phase_cu() {
 }
 
 // Workgroups per CU the launch bounds ask for: 8 waves in all, unless the two K and V tiles
-// (8*KT*DP bytes of LDS) or the O and Q registers (DP > 128) allow only one workgroup.
+// (8*KT*DP bytes of LDS), the O and Q registers (DP > 128) or the workgroup's own size (12
+// waves) allow only one workgroup.
 constexpr int prefill_wg_per_cu(int DP, int KT, int NW) {
-    return (DP > 128 || 8 * KT * DP > 80 * 1024) ? 1 : 8 / NW;
+    return (DP > 128 || 8 * KT * DP > 80 * 1024 || NW > 8) ? 1 : 8 / NW;
 }
 
 // KH (key halves, NW = 8): a workgroup of 4 * 32 query rows whose waves w and w + 4 take the
 // same rows and the two halves of every key tile (KW = KT / 2 keys each, one wave of each SIMD
 // per half), combined through LDS at the end. For grids too small for one 256-row workgroup
 // per CU, this keeps two waves per SIMD and 128-key tiles where 4-wave workgroups would take
-// 64-key tiles.
+// 64-key tiles. NW = 12 (DP = 64, non-causal, packed rows): 6 * 32 rows per workgroup, waves
+// w and w + 6 on the same rows, three waves per SIMD; one such workgroup per CU holds the
+// rows of one and a half 128-row tiles with no partials to merge.
 template <int DP, int KT, int NW, bool CAUSAL, bool VT, bool KH>
 __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_prefill_fast_kernel(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
@@ -524,7 +527,9 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     int hsplit) {
     // D <= DP, D % 8 == 0: head-dim columns D .. DP-1 of the tiles and of Q are zero.
     static_assert(DP % 32 == 0 && KT % 32 == 0, "tile shape");
-    static_assert(!KH || (NW == 8 && KT == 128 && DP >= 64), "key halves: 8 waves, 128-key tiles");
+    static_assert(!KH || (KT == 128 && ((NW == 8 && DP >= 64) || (NW == 12 && DP == 64 && !CAUSAL))),
+                  "key halves: 8 waves (or 12 at DP = 64), 128-key tiles");
+    static_assert(NW != 12 || KH, "12 waves: key halves only");
     constexpr int NR = KH ? NW / 2 : NW; // waves with distinct query rows
     constexpr int KW = KH ? KT / 2 : KT; // keys of a tile that one wave takes
     constexpr int BQ = NR * 32;         // query rows per workgroup
@@ -532,6 +537,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     __shared__ __attribute__((aligned(1024))) uint16_t Ks[2][KT * DP];
     __shared__ __attribute__((aligned(1024))) uint16_t Vs[2][KT * DP];
     __shared__ float kh_ml[KH ? 2 * NR * 64 : 1]; // KH: (m, l) of each second-half lane
+    // KH: the second halves' o go to the buffer pair the last tile left idle (4 * KT * DP bytes,
+    // KT / 32 waves' (DP / 32) * 16 * 64 floats) where they fit, else to an area of their own.
+    constexpr int KHO = (KH && NR * DP * 32 * 4 > 4 * KT * DP) ? NR * DP * 32 : 1;
+    __shared__ float kh_o[KHO];
 
     const int g = Hq / Hkv;
     const int L0 = xcd_remap_paired(wg_id_x(), nwg, pair_r); // nwg: the grid's workgroup count
@@ -660,7 +669,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     constexpr int QSWZ = (NQC % 16 == 0) ? 15 : ((NQC % 8 == 0) ? 7 : 3);
     const bool qstage = NW == 8 && KT >= 16 * NW && DP <= 128 && !pack &&
                         (long)Sq * D * 2 < 0x7fffffffL;
-    const uint16_t *qlds = (w < NW / 2 ? &Ks[1][0] : &Vs[1][0]) + (w % (NW / 2)) * 32 * DP;
+    const uint16_t *qlds =
+        NW == 8 ? (w < NW / 2 ? &Ks[1][0] : &Vs[1][0]) + (w % (NW / 2)) * 32 * DP : &Ks[1][0];
     if (qstage) {
         const __amdgpu_buffer_rsrc_t rq =
             make_rsrc(Q + (size_t)h * Sq * D, (uint32_t)Sq * (uint32_t)D * 2u);
@@ -975,7 +985,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     auto tile_pipelined = [&](int buf) __attribute__((always_inline)) {
         constexpr int NS = KW / 32;
         constexpr int NDB = DP / 32, NKK = DP / 16;
-        const uint16_t *kb0 = &Ks[buf][kfo];
+        const uint16_t *kb0 = &Ks[buf][kfo + kh * (KW / 32) * KSUB];
         bf16x8 ka[2][NKK];
         float mc = m_run * c; // m_run is finite: every row of the wave has had an admissible key
 #pragma unroll
@@ -1038,7 +1048,8 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
 #pragma unroll
                 for (int m = 0; m < NMF; ++m) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, (NDS + NMF - 1) / NMF, 0);
+                    if constexpr (NDS > 0)
+                        __builtin_amdgcn_sched_group_barrier(0x100, (NDS + NMF - 1) / NMF, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 64 / NMF, 0);
                 }
             }
@@ -1115,9 +1126,10 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
                           ((kbase + KW > Sk) || (CAUSAL && kbase + KW - 1 > Sk - Sq + qmin));
         if (kbase <= wave_maxkey) {
             // The pipelined path at DP <= 64 only: at larger DP it spills (two sub-tiles' K
-            // fragments, S and the V read-ahead do not fit beside O and Q).
-            if (DP <= 64 && !KH && !decltype(first)::value && !edge && pipe) {
-                if constexpr (DP <= 64 && !KH)
+            // fragments, S and the V read-ahead do not fit beside O and Q). Key halves take it
+            // on 12 waves only (two 32-key sub-tiles per wave).
+            if (DP <= 64 && (!KH || NW == 12) && !decltype(first)::value && !edge && pipe) {
+                if constexpr (DP <= 64 && (!KH || NW == 12))
                     tile_pipelined(buf);
             } else {
                 qk(buf);
@@ -1166,14 +1178,16 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
     if constexpr (KH) {
         // The second-half wave of each row block hands its (m, l, o) to the first-half wave
         // through LDS: o into the buffer pair the last tile left idle ((kt1 - kt0) & 1: past
-        // the barrier after its last reader, no DMA pending), 16-byte pieces in lane order, so
+        // the barrier after its last reader, no DMA pending; 12 waves: kh_o), 16-byte pieces in
+        // lane order, so
         // each lane reads back exactly its partner lane's values (same query, same d, same key
         // parity). After the barrier the first-half wave combines the two with log-sum-exp
         // weights against the larger m (a half with no admissible key has m = -inf, weight 0),
         // and only it goes on to the epilogue, which then stages O in the other buffer.
         const int nbx = (kt1 - kt0) & 1;
-        float *xo = reinterpret_cast<float *>((wr & 2) ? &Vs[nbx][0] : &Ks[nbx][0]) +
-                    (wr & 1) * (DP / 32) * 16 * 64;
+        float *xo = (KHO > 1) ? &kh_o[wr * DP * 32]
+                              : reinterpret_cast<float *>((wr & 2) ? &Vs[nbx][0] : &Ks[nbx][0]) +
+                                    (wr & 1) * (DP / 32) * 16 * 64;
         if (kh == 1) {
             kh_ml[wr * 128 + lane] = m_run;
             kh_ml[wr * 128 + 64 + lane] = l_run;
@@ -2912,6 +2926,23 @@ static int prefill_head_split(int Hq, int Sq, int nqt, int nkt, long slots, bool
     return (int)hs;
 }
 
+// Non-causal grids at DP = 64 that take the head split may run instead as 12-wave key-halves
+// workgroups of 192 rows (attn_prefill_fast_kernel, NW = 12), a kv head's g * Sq query rows
+// tiled as one row space, one workgroup per CU, where they fit one round: each CU then holds
+// at most 192 rows, as with the head split's one and a half 128-row tiles, but with three waves
+// per SIMD, no partials to write and no merge kernel.
+// ATTN_PREFILL_W12=0 (read once) keeps the head split for tuning sweeps.
+static bool prefill_rows192(int Hq, int Hkv, int Sq) {
+    static int env = -1;
+    if (env < 0) {
+        const char *e = getenv("ATTN_PREFILL_W12");
+        env = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    const long nwg = (long)Hkv * (((long)(Hq / Hkv) * Sq + 191) / 192);
+    return env && device_cus() % 8 == 0 && nwg <= device_cus() &&
+           (long)(Hq / Hkv) * Sq < 0x7fffffffL;
+}
+
 // A causal grid of at most one workgroup per CU is as slow as its heaviest query tile. Then the
 // key range of each tile in the upper half (qt >= nqt/2) is split in two workgroups whose
 // partials (m, l, acc) go to the caller's scratch and are merged, when the slots suffice.
@@ -2921,7 +2952,7 @@ hipError_t launch_prefill_fast_nw(const uint16_t *Q, const uint16_t *K, const ui
                                   float *pm, float *pl, float *pacc, long slots, hipStream_t st) {
     constexpr int BQ = (KH ? NW / 2 : NW) * 32;
     const int g = Hq / Hkv;
-    const int pack = prefill_pack(Hq, Hkv, Sq) ? 1 : 0;
+    const int pack = (NW == 12 || prefill_pack(Hq, Hkv, Sq)) ? 1 : 0; // 12 waves: packed rows
     const int nqt = pack ? (g * Sq + BQ - 1) / BQ : (Sq + BQ - 1) / BQ;
     long nblk = (long)(pack ? Hkv : Hq) * nqt;
     const int nsplit = prefill_key_split(nblk, prefill_wg_per_cu(DP, KT, NW), (Sk + KT - 1) / KT,
@@ -3155,6 +3186,11 @@ hipError_t launch_prefill_fast_t(const uint16_t *Q, const uint16_t *K, const uin
     const bool hs = !CAUSAL && DP <= 64 && !prefill_pack(Hq, Hkv, Sq) &&
                     prefill_head_split(Hq, Sq, (Sq + 127) / 128, (Sk + KT4 - 1) / KT4,
                                        pm ? slots : 0, pm != nullptr) > 0;
+    if constexpr (DP == 64 && KT == 128 && !CAUSAL)
+        if (hs && !prefill_waves_forced() && prefill_rows192(Hq, Hkv, Sq))
+            return launch_prefill_fast_nw<DP, KT, 12, CAUSAL, VT, true>(Q, K, V, O, Hq, Hkv, Sq, Sk,
+                                                                        D, c, pm, pl, pacc, slots,
+                                                                        st);
     const int nw = (DP <= 128) ? prefill_waves(Hq, Hkv, Sq, Sk, CAUSAL, hs) : 4;
     // Tuning override of the key tile (the other of 64 / 128 keys), non-V^T only; the counter
     // study that fixed the defaults runs through it.
