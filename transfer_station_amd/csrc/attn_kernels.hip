@@ -174,7 +174,31 @@ __device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf
 
 // max(x[lane], x[lane ^ 32]), through ds_bpermute (compiler-managed waits). The row max runs on
 // an item's first key tile and on rare recomputed tiles only, so the exchange's cost is small.
-__device__ __forceinline__ float max_xor32(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+// Lane exchanges of a value with lane l ^ 16 or l ^ 32 on the VALU (v_permlane16_swap /
+// v_permlane32_swap with the value as both operands), where __shfl_xor goes through the LDS
+// crossbar and its wait (lgkmcnt) also waits for the wave's LDS reads in flight. Each lane gets
+// the pair {its value, its partner's} in one order or the other, so max and sum (commutative)
+// give exactly what fmaxf / + with the shuffled value give.
+__device__ __forceinline__ float max_xor32(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
+}
 
 __device__ __forceinline__ void lds_wave_fence() {
     // Wave-private LDS reuse: finish this wave's outstanding LDS traffic and keep the compiler
@@ -330,7 +354,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
                     mx = fmaxf(mx, s[t][i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = max_xor32(mx);
             const float mnew = fmaxf(m_run, mx);
             const float muse = (mnew == kNegInf) ? 0.f : mnew;
             const float alpha = fast_exp2((m_run - muse) * c);
@@ -380,7 +404,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
         __syncthreads();
     }
 
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = sum_xor32(l_run);
     const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
     if (myq < Sq) {
         float *orow = O + ((size_t)h * Sq + myq) * D;
@@ -1220,7 +1244,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
             }
     }
     phase_stamp(w, lane, 4);
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = sum_xor32(l_run);
     if (part >= 0 || nsplit > 1) {
         // Unnormalised partial of one key range: (m, l, acc) into slot (row, part) for the
         // log-sum-exp merge (attn_merge2_kernel / attn_merge_kernel).
@@ -1695,7 +1719,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_persist_kernel(
     // ordinary policy measured within 1%), where they evicted the K/V tiles of the next items;
     // non-temporal partial lines were written back piecemeal (2.35x the bytes).
     auto store_o = [&](int h, int qt, bool valid) __attribute__((always_inline)) {
-        const float lt = l_run + __shfl_xor(l_run, 32);
+        const float lt = sum_xor32(l_run);
         const float inv = (lt > 0.f) ? 1.0f / lt : 0.f;
         const __amdgpu_buffer_rsrc_t ro = make_rsrc(O + (size_t)h * Sq * D, 2u * qbytes);
         int r = wr * 32 + (lane & 7);
@@ -2142,8 +2166,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
                     s[t][i] = kNegInf;
                 mx = fmaxf(mx, s[t][i]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_xor32(max_xor16(mx));
         const float mnew = fmaxf(m_run, mx);
         const float muse = (mnew == kNegInf) ? 0.f : mnew;
         const float alpha = fast_exp2((m_run - muse) * c);
@@ -2182,8 +2205,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
             }
         }
     }
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_xor32(sum_xor16(l_run));
 
     // Merge the 4 waves: O^T register (db, i) of this lane holds d = 16db + 4grp + i, row r16.
     __syncthreads();
@@ -2381,8 +2403,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
                             s[t][x] = kNegInf;
                         mx = fmaxf(mx, s[t][x]);
                     }
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = max_xor32(max_xor16(mx));
                 const float mnew = fmaxf(m_run, mx);
                 const float muse = (mnew == kNegInf) ? 0.f : mnew;
                 alc[i] = fast_exp2((m_run - muse) * c);
@@ -2436,8 +2457,7 @@ __global__ __launch_bounds__(256, 2) void attn_decode_vt_kernel(
         livep = livec;
         livec = 0;
     }
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    l_run = sum_xor32(sum_xor16(l_run));
 
     // Merge the 4 waves (as attn_decode_kernel): O^T register (db, i) holds d = 16db + 4grp + i.
     __syncthreads();
