@@ -456,7 +456,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 //     tiles, each lane carrying its own head and query index.
 //   * grids that do not fill the GPU evenly: a key split over several workgroups (partials
 //     merged by attn_mergew_kernel), the slot-balanced head split (D <= 64: whole tiles and key
-//     halves placed by XCD position), and key halves inside one workgroup (KH, D > 64).
+//     halves placed by XCD position), and key halves inside one workgroup (KH: 8 waves at
+//     D >= 64; 12 waves over 192 packed rows at D <= 64, in place of the head split where such
+//     workgroups fit one per CU).
 // ------------------------------------------------------------------------------------------
 // Bound on a lane's tile sum of p = 2^(s c - m c) taken against a stale m (and so on each p).
 // 2^16: on peaked rows (config 5's Q ~ N(0, 16)) a cap of 2^8 / 2^12 / 2^16 sends 9.9% / 2.2% /
