@@ -1186,7 +1186,7 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         // wave's first row); the loop before them has no mask code. Measured (same box) on the
         // 4-wave 64-key-tile kernels: c3 1k causal +3.3%, Qwen3 4k causal +2.8%, 32 heads 2k
         // causal +2%, 16 heads 2k +1.5%, others within 0.5%. The 8-wave kernels lost 1.5-3.5%
-        // with it (c3 4k, c3 causal, c4) and the D = 64 ones 1-2.4%, so they keep one loop.
+        // with it (c3 4k, c3 causal, c4), so they keep one loop (at D <= 64 see below).
         const int medge = CAUSAL ? min(Sk - KT, Sk - Sq + qmin - KT + 1) : Sk - KT;
         const int kt_e = __builtin_amdgcn_readfirstlane(medge < 0 ? 0 : medge / KT + 1);
         int kt = kt0 + 1;
@@ -1195,7 +1195,34 @@ __global__ __launch_bounds__(NW * 64, prefill_wg_per_cu(DP, KT, NW)) void attn_p
         for (; kt < kt1; ++kt)
             step(kt, std::false_type{}, std::true_type{});
     } else {
-        for (int kt = kt0 + 1; kt < kt1; ++kt)
+        int kt = kt0 + 1;
+        if constexpr (DP <= 64 && (!KH || NW == 12)) {
+            // A wave with query rows runs its tiles before kt_e (no mask needed) in a loop of
+            // their own whose body is the pipelined tile alone: with the general tile path in
+            // the same loop body, the register allocator kept o in different registers on the
+            // two paths and copied it in and out of each pipelined tile (36 v_mov per 64 keys on
+            // 12 waves, 18 per 128 on 4 or 8). Bit-identical; same box: config 5 61.6 -> 56.2 us,
+            // 40 heads of 1000 rows over 4000 keys +12%, D = 40 +11%, 128 heads at 1k +4.3%,
+            // the head split's 4-wave grid +3.7%, 64 heads at 2k causal +3.1%.
+            const int medge = CAUSAL ? min(Sk - KT, Sk - Sq + qmin - KT + 1) : Sk - KT;
+            const int kt_e = __builtin_amdgcn_readfirstlane(medge < 0 ? 0 : medge / KT + 1);
+            if (pipe && __builtin_amdgcn_readfirstlane(wave_maxkey) >= 0) {
+                for (; kt < min(kt1, kt_e); ++kt) {
+                    const int buf = (kt - kt0) & 1;
+                    if (kt + 1 < kt1) {
+                        dma_k(kt + 1, buf ^ 1);
+                        dma_v(kt + 1, buf ^ 1);
+                    }
+                    tile_pipelined(buf);
+                    // The same wait and barrier as the end of step().
+                    if (kt + 1 < kt1) {
+                        __builtin_amdgcn_s_waitcnt(0x0F70);
+                        __syncthreads();
+                    }
+                }
+            }
+        }
+        for (; kt < kt1; ++kt)
             step(kt, std::false_type{}, std::true_type{});
     }
     phase_stamp(w, lane, 3);
